@@ -1,0 +1,135 @@
+/*
+ * tinyserve_amd.h: the C ABI of libtinyserve_amd.so, the MI355X (gfx950) kernels of
+ * TinyServe's attention hot path.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes, launches
+ * on the given HIP stream (a hipStream_t passed as void*; NULL = the null stream) and
+ * returns without synchronising, so each call may be captured into a HIP graph. The
+ * library never allocates device memory: outputs and split-K partials are owned by the
+ * caller. Return value: 0 on success, a negative TS_E* code for an argument the kernels
+ * cannot take (nothing was launched), or a positive hipError_t from the launch.
+ *
+ * Strides are in ELEMENTS of the tensor they describe. The last (head_dim) dimension of
+ * every tensor must be contiguous. Layouts follow the reference:
+ *   q / out (decode)   [B, Hq, D]            (stride_b, stride_h, 1)
+ *   q / out (prefill)  [T, Hq, D]            (stride_t, stride_h, 1)
+ *   k_cache, v_cache   [num_slots, Hkv, D]   one layer; (stride_slot, stride_head, 1)
+ *   block_tables       [B or R, W] int32     row stride bt_stride
+ *   slot of position p = block_tables[row, p / block_size] * block_size + p % block_size
+ */
+#ifndef TINYSERVE_AMD_H
+#define TINYSERVE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types. */
+enum ts_dtype { TS_F32 = 0, TS_F16 = 1, TS_BF16 = 2 };
+
+/* Negative return codes (argument errors, detected before any launch). */
+#define TS_EINVAL (-1)      /* sizes or strides that do not fit together */
+#define TS_EUNSUPPORTED (-2) /* a shape/dtype combination with no compiled kernel */
+
+/* Library version, (major << 16) | minor. */
+int ts_version(void);
+
+/* Text for a return code of any entry point. */
+const char* ts_strerror(int code);
+
+/*
+ * Paged GQA decode attention, one pass of split-K.
+ *
+ * Replaces the launches of _paged_decode_kernel, _paged_decode_grouped_kernel and
+ * _paged_decode_split_kernel (reference src/tinyserve/triton_attention.py:76, :193,
+ * :243), issued by launch_paged_decode (:394), launch_paged_decode_grouped (:447) and
+ * launch_paged_decode_split (:534).
+ *
+ * One wavefront per (sequence, tile of `head_tile` query heads, split). Query head h reads
+ * kv head h / (Hq / Hkv). head_tile = 1 is the per-query-head launch shape of
+ * _paged_decode_kernel (any Hq / Hkv); head_tile = 0 picks the whole GQA group (it
+ * needs Hq / Hkv to be a power of 2).
+ *
+ * Sequence b's blocks 0 .. ceil(lens[b] / block_size) - 1 are cut into `splits`
+ * contiguous ranges of ceil(nblocks / splits) blocks (the reference's ranges,
+ * triton_attention.py:283-286). splits == 1: `out` [B, Hq, D] receives the normalised
+ * result in the q dtype and m/l/acc are not touched (may be NULL). splits > 1: every range
+ * writes its fp32 partial to m, l [B, Hq, splits] and acc [B, Hq, splits, D]
+ * (contiguous, part index (b * Hq + h) * splits + split); `out` is not touched, and
+ * ts_decode_combine finishes the result. m is stored in base-2 units (log2 e * max score).
+ */
+int ts_decode_split(const void* q, const void* k_cache, const void* v_cache,
+                    const int32_t* block_tables, const int32_t* context_lens, void* out,
+                    float* m, float* l, float* acc, int B, int Hq, int Hkv, int D,
+                    int block_size, int64_t q_stride_b, int64_t q_stride_h,
+                    int64_t o_stride_b, int64_t o_stride_h, int64_t k_stride_slot,
+                    int64_t k_stride_head, int64_t bt_stride, int splits, int head_tile,
+                    float scale, int dtype, void* stream);
+
+/*
+ * The split-K combine pass: out[b, h] = sum_s w_s acc_s / sum_s w_s l_s with
+ * w_s = 2^(m_s - max_s m_s); an empty range (m = -inf, l = 0) weighs 0.
+ * Replaces _merge_splits_kernel (triton_attention.py:299-327).
+ */
+int ts_decode_combine(const float* m, const float* l, const float* acc, void* out, int B,
+                      int Hq, int D, int64_t o_stride_b, int64_t o_stride_h, int splits,
+                      int dtype, void* stream);
+
+/*
+ * Varlen causal prefill attention over the paged cache.
+ * Replaces _paged_prefill_kernel as launched by paged_prefill_attention
+ * (reference src/tinyserve/triton_prefill.py:50-125, :128-216).
+ *
+ * Sequence r's queries are rows q_starts[r] .. q_starts[r] + q_lens[r] - 1 of q and
+ * are its positions context_lens[r] - q_lens[r] .. context_lens[r] - 1; query at
+ * position p attends keys 0 .. p of its own block table. Only those rows of `out`
+ * are written. max_q_len (>= every q_lens entry) sizes the grid without a host sync.
+ * fp16/bf16 with head_dim 64 or 128 run on MFMA and round the softmax weights to the
+ * input dtype before P.V (as the reference kernel does, triton_prefill.py:118); other
+ * shapes and fp32 use fp32 FMA throughout.
+ */
+int ts_prefill_varlen(const void* q, const void* k_cache, const void* v_cache, void* out,
+                      const int32_t* block_tables, const int32_t* q_starts,
+                      const int32_t* q_lens, const int32_t* context_lens, int R, int Hq,
+                      int Hkv, int D, int block_size, int max_q_len, int64_t q_stride_t,
+                      int64_t q_stride_h, int64_t o_stride_t, int64_t o_stride_h,
+                      int64_t k_stride_slot, int64_t k_stride_head, int64_t bt_stride,
+                      float scale, int dtype, void* stream);
+
+/*
+ * RMSNorm of every row of x [T, N]:
+ *   out = (T)(x * 1/sqrt(mean(x^2) + eps)) * w   (normalise in fp32, multiply in T)
+ * Replaces _rms_norm_rows_kernel / rms_norm_rows (triton_fused.py:29-40, :116-126).
+ * x, w and out share `dtype`. T == 0 launches nothing.
+ */
+int ts_rms_norm_rows(const void* x, const void* w, void* out, int T, int N,
+                     int64_t x_stride, int64_t o_stride, float eps, int dtype, void* stream);
+
+/*
+ * Per-head RMSNorm + rotate-half RoPE of q and k, and the paged KV-cache write.
+ * Replaces _qk_norm_rope_store_kernel / qk_norm_rope_store (triton_fused.py:43-113,
+ * :129-177).
+ *   q_out[t, h]             = rope(norm(q[t, h]) * q_w)                    (h < Hq)
+ *   k_cache[slots[t], kh]   = (cache dtype)(rope(norm(k[t, kh]) * k_w))
+ *   v_cache[slots[t], kh]   = (cache dtype)v[t, kh]                         (exact copy)
+ * rope(a, b) on the halves: (a cos - b sin, b cos + a sin) with cos/sin [T, D] fp32,
+ * of which only columns 0 .. D/2 - 1 are read. q, k, v, weights and q_out share
+ * `dtype`; both caches share `cache_dtype`. slots are int64.
+ */
+int ts_qk_norm_rope_store(const void* q, const void* k, const void* v, void* q_out,
+                          const void* q_weight, const void* k_weight, const float* cos,
+                          const float* sin, const int64_t* slots, void* k_cache,
+                          void* v_cache, int T, int Hq, int Hkv, int D, int64_t q_stride_t,
+                          int64_t q_stride_h, int64_t k_stride_t, int64_t k_stride_h,
+                          int64_t v_stride_t, int64_t v_stride_h, int64_t o_stride_t,
+                          int64_t o_stride_h, int64_t cs_stride_t, int64_t c_stride_slot,
+                          int64_t c_stride_head, float eps, int dtype, int cache_dtype,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TINYSERVE_AMD_H */

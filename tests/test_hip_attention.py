@@ -1,0 +1,220 @@
+"""The HIP paged decode-attention kernels must match the oracle (GPU).
+
+Mirrors the reference's tests/test_triton_attention.py and tests/test_kernel_variants.py
+case by case, with the oracle's ``decode_ref`` (a restatement of
+``paged_decode_attention_ref``, attention.py:114-141) as the reference. Every cache slot
+no sequence owns is NaN and block-table padding points at a NaN block, so a kernel that
+reads one slot too many returns NaN and fails. Tolerances: tests/helpers.py.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable
+
+import pytest
+import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from oracle import ref
+from tests.helpers import TOL, assert_matches
+from tinyserve_amd import hip_attention as ha
+from tinyserve_amd.workloads import DecodeCase, decode_bench_case, decode_case
+
+pytestmark = pytest.mark.gpu
+DEVICE = "cuda"
+KERNELS = [ha.paged_decode_attention, ha.paged_decode_attention_grouped, ha.paged_decode_attention_split]
+
+
+def on_gpu(c: DecodeCase) -> DecodeCase:
+    return DecodeCase(*(t.to(DEVICE) for t in c.args()), c.scale, c.block_size)
+
+
+def oracle32(c: DecodeCase) -> torch.Tensor:
+    """The oracle's float32 result (before rounding to the case's dtype)."""
+    return ref.decode_ref(c.q.float(), c.k_cache.float(), c.v_cache.float(), c.block_tables,
+                          c.context_lens, c.scale, c.block_size)  # fmt: skip
+
+
+def check(c: DecodeCase, kernels: list[Callable[..., torch.Tensor]] = KERNELS) -> torch.Tensor:
+    want = oracle32(c)
+    g = on_gpu(c)
+    for kernel in kernels:
+        out = kernel(*g.args(), g.scale, g.block_size)
+        assert out.dtype == c.q.dtype and out.device.type == "cuda"
+        assert torch.isfinite(out).all(), f"{kernel.__name__}: read a slot outside the sequence"
+        assert_matches(out, want, c.q.dtype, kernel.__name__)
+    return want
+
+
+def test_one_token_returns_its_value() -> None:
+    c = decode_case([1], num_q_heads=4, num_kv_heads=2, head_dim=32)
+    out = ha.paged_decode_attention_split(*on_gpu(c).args(), c.scale, c.block_size)
+    slot = int(c.block_tables[0, 0]) * c.block_size
+    torch.testing.assert_close(out[0].cpu(), c.v_cache[slot].repeat_interleave(2, dim=0),
+                               atol=1e-6, rtol=1e-6)  # fmt: skip
+    check(c)
+
+
+def test_qwen3_shapes_across_block_boundaries() -> None:
+    check(decode_case([1, 15, 16, 17, 31, 32, 33, 193]))
+
+
+def test_baseline_config_1() -> None:
+    # fp32, 16/8/128, contexts {17, 64, 128, 200}, a 64-block pool.
+    check(decode_case([17, 64, 128, 200], pool_blocks=64))
+
+
+@pytest.mark.parametrize(("num_q_heads", "num_kv_heads"), [(4, 4), (8, 2), (8, 1), (16, 2)])
+def test_head_groupings(num_q_heads: int, num_kv_heads: int) -> None:
+    check(decode_case([3, 20, 47], num_q_heads, num_kv_heads, head_dim=64))
+
+
+def test_a_group_that_is_not_a_power_of_2_on_the_per_head_kernel() -> None:
+    check(decode_case([3, 40], 12, 4, head_dim=32), [ha.paged_decode_attention])
+
+
+@pytest.mark.parametrize("block_size", [1, 2, 8, 32, 64])
+def test_block_sizes(block_size: int) -> None:
+    check(decode_case([1, 9, 40, 130], 4, 2, head_dim=32, block_size=block_size))
+
+
+@pytest.mark.parametrize("head_dim", [8, 16, 32, 64, 128, 256])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_head_dims_and_dtypes(head_dim: int, dtype: torch.dtype) -> None:
+    if head_dim * (4 if dtype == torch.float32 else 2) < 16:
+        pytest.skip("rows under 16 bytes are not a kernel shape")
+    check(decode_case([1, 33, 90], 4, 2, head_dim=head_dim, dtype=dtype, seed=head_dim))
+
+
+def test_float16() -> None:
+    check(decode_case([1, 16, 100, 193], dtype=torch.float16))
+
+
+def test_bfloat16() -> None:
+    check(decode_case([1, 16, 100, 193], dtype=torch.bfloat16))
+
+
+def test_large_scores_do_not_overflow() -> None:
+    check(decode_case([40, 70], 4, 2, head_dim=64, dtype=torch.float16, magnitude=12.0))
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_each_sequence_only_sees_its_own_blocks(kernel: Callable[..., torch.Tensor]) -> None:
+    # Running sequences together or alone gives the same rows, bit for bit.
+    c = on_gpu(decode_case([7, 30, 2], 4, 2, head_dim=32, block_size=4))
+    together = kernel(*c.args(), c.scale, c.block_size)
+    for b in range(3):
+        alone = kernel(c.q[b : b + 1], c.k_cache, c.v_cache, c.block_tables[b : b + 1],
+                       c.context_lens[b : b + 1], c.scale, c.block_size)  # fmt: skip
+        assert torch.equal(alone, together[b : b + 1])
+
+
+@settings(max_examples=15, deadline=None)
+@given(
+    lens=st.lists(st.integers(1, 70), min_size=1, max_size=4),
+    heads=st.sampled_from([(2, 1), (4, 2), (4, 4)]),
+    head_dim=st.sampled_from([16, 32]),
+    block_size=st.sampled_from([2, 4, 16]),
+    seed=st.integers(0, 2**16),
+)
+def test_random_shapes(lens: list[int], heads: tuple[int, int], head_dim: int, block_size: int,
+                       seed: int) -> None:  # fmt: skip
+    check(decode_case(lens, *heads, head_dim=head_dim, block_size=block_size, seed=seed))
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 5, 16])
+@pytest.mark.parametrize("lens", [[1], [17, 300, 33], [64, 2]])
+def test_any_number_of_splits_gives_the_same_result(splits: int, lens: list[int]) -> None:
+    # More ranges than a sequence has blocks leaves some empty: they must not count.
+    c = decode_case(lens, 4, 2, head_dim=32, block_size=4, seed=splits)
+    want = oracle32(c)
+    g = on_gpu(c)
+    out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, num_splits=splits)
+    assert torch.isfinite(out).all()
+    assert_matches(out, want, torch.float32)
+
+
+@pytest.mark.parametrize("tile", [(1, 2), (2, 4), (4, 8), (8, 8)])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_every_tile_gives_the_same_result(tile: tuple[int, int], splits: int) -> None:
+    c = decode_case([17, 300, 33], 4, 2, head_dim=32, block_size=4, seed=tile[0] + splits)
+    want = oracle32(c)
+    g = on_gpu(c)
+    out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, splits, tile)
+    assert_matches(out, want, torch.float32)
+    grouped = ha.launch_paged_decode_grouped(*g.args(), c.scale, c.block_size, tile)
+    assert_matches(grouped, want, torch.float32)
+
+
+WIDTHS = [1, 2, 9, 16, 32]
+
+
+def widened(tables: torch.Tensor, width: int) -> torch.Tensor:
+    """``tables`` cut or padded to ``width`` columns (padding repeats the NaN block)."""
+    if width <= tables.shape[1]:
+        return tables[:, :width].contiguous()
+    pad = tables[:, -1:].expand(-1, width - tables.shape[1])
+    return torch.cat([tables, pad], dim=1).contiguous()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_every_width_and_split_count_gives_the_reference(dtype: torch.dtype) -> None:
+    # test_kernel_variants.py:44-58: every block-table width and every split count.
+    c = decode_case([5, 12, 16], dtype=dtype, seed=7)
+    want = oracle32(c)
+    g = on_gpu(c)
+    for w in WIDTHS:
+        args = (g.q, g.k_cache, g.v_cache, widened(g.block_tables, w), g.context_lens)
+        for launch in (ha.launch_paged_decode, ha.launch_paged_decode_grouped):
+            assert_matches(launch(*args, c.scale, c.block_size), want, dtype, f"w={w}")
+        for s in range(2, ha.MAX_SPLITS + 1):
+            out = ha.launch_paged_decode_split(*args, c.scale, c.block_size, num_splits=s)
+            assert_matches(out, want, dtype, f"w={w} s={s}")
+
+
+def test_thirty_two_sequences_at_qwen3_shapes() -> None:
+    # test_triton_attention.py:304-311: the C=32 step, 32 sequences of ~161 tokens, fp16.
+    c = decode_case([161 + i for i in range(32)], dtype=torch.float16, seed=3)
+    want = oracle32(c)
+    g = on_gpu(c)
+    for splits in (None, 1, 4):
+        out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, splits)
+        assert_matches(out, want, torch.float16, f"splits={splits}")
+
+
+def test_one_long_sequence() -> None:
+    check(decode_case([2048], dtype=torch.float16, seed=2))
+
+
+def test_benchmark_sized_batch() -> None:
+    check(decode_case([193] * 64, dtype=torch.float16, seed=1))
+
+
+def test_baseline_config_2() -> None:
+    # fp16, B=32 at context 256, a 4096-block pool, 4 splits + combine.
+    c = decode_case([256] * 32, dtype=torch.float16, pool_blocks=4096, seed=0)
+    want = oracle32(c)
+    g = on_gpu(c)
+    out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, num_splits=4)
+    assert torch.isfinite(out).all()
+    assert_matches(out, want, torch.float16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_metric_size_batch(dtype: torch.dtype) -> None:
+    # The metric's workload, B=64 x 4096, fp16/bf16: 8 of the 64 sequences against the
+    # oracle, every sequence for split-count invariance (1 vs 8 vs 16 splits).
+    c = decode_bench_case(64, 4096, dtype=dtype, seed=5)
+    outs = {s: ha.launch_paged_decode_split(*c.args(), c.scale, c.block_size, num_splits=s)
+            for s in (1, 8, 16)}  # fmt: skip
+    for s, out in outs.items():
+        assert torch.isfinite(out).all(), s
+    tol = TOL[dtype] * 2
+    torch.testing.assert_close(outs[8], outs[1], atol=tol, rtol=tol)
+    torch.testing.assert_close(outs[16], outs[1], atol=tol, rtol=tol)
+    kc, vc = c.k_cache.cpu(), c.v_cache.cpu()
+    for b in range(0, 64, 8):
+        sub = DecodeCase(c.q[b : b + 1].cpu(), kc, vc, c.block_tables[b : b + 1].cpu(),
+                         c.context_lens[b : b + 1].cpu(), c.scale, c.block_size)  # fmt: skip
+        assert_matches(outs[8][b : b + 1], oracle32(sub), dtype, f"seq {b}")

@@ -1,0 +1,188 @@
+"""The C-ABI library and the host side of the entry points, on the CPU.
+
+The library is loaded (never asked to launch): every function ``include/tinyserve_amd.h``
+declares must be exported and bound. The Python entry points must raise the reference's
+ValueErrors before touching the device, and must refuse CPU tensors outright (no CPU
+fallback) once the arguments are valid.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from tinyserve_amd import _lib, hip_attention, hip_fused, hip_prefill
+from tinyserve_amd.workloads import decode_case, prefill_case
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tinyserve_amd.h"
+
+
+@pytest.fixture(scope="module")
+def lib() -> ctypes.CDLL:
+    if not _lib.LIB_PATH.exists():
+        from tinyserve_amd.build import build
+
+        build()
+    return _lib.load()
+
+
+def declared() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"\b(ts_[a-z_0-9]+)\s*\(", text)
+
+
+def test_header_declares_what_the_binding_binds() -> None:
+    assert sorted(declared()) == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib: ctypes.CDLL) -> None:
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert lib.ts_version() == (0 << 16) | 1
+    assert b"invalid argument" in lib.ts_strerror(-1)
+    assert b"unsupported" in lib.ts_strerror(-2)
+
+
+def test_c_abi_rejects_bad_sizes_before_any_launch(lib: ctypes.CDLL) -> None:
+    # Hq not a multiple of Hkv, a block size that is not a power of 2, zero splits: the
+    # library returns TS_EINVAL without launching (null pointers are never touched).
+    null = None
+    strides = (0,) * 7
+    assert lib.ts_decode_split(*([null] * 9), 1, 6, 4, 32, 16, *strides, 1, 0, 1.0, 0, null) == -1
+    assert lib.ts_decode_split(*([null] * 9), 1, 4, 2, 32, 12, *strides, 1, 0, 1.0, 0, null) == -1
+    assert lib.ts_decode_split(*([null] * 9), 1, 4, 2, 32, 16, *strides, 0, 0, 1.0, 0, null) == -1
+    # splits > 1 needs the partial buffers
+    assert lib.ts_decode_split(*([null] * 9), 1, 4, 2, 32, 16, *strides, 2, 0, 1.0, 0, null) == -1
+    assert lib.ts_prefill_varlen(*([null] * 8), 1, 12, 4, 32, 16, 4, *strides, 1.0, 0, null) == -1
+    assert lib.ts_rms_norm_rows(null, null, null, 4, 0, 0, 0, 1e-6, 0, null) == -1
+    assert lib.ts_qk_norm_rope_store(*([null] * 11), 1, 4, 2, 12, *([0] * 11), 1e-6, 0, 0, null) == -1
+    # empty batches launch nothing and succeed
+    assert lib.ts_decode_split(*([null] * 9), 0, 4, 2, 32, 16, *strides, 1, 0, 1.0, 0, null) == 0
+    assert lib.ts_rms_norm_rows(null, null, null, 0, 16, 16, 16, 1e-6, 1, null) == 0
+
+
+# --- decode entry points: the reference's argument errors (test_triton_attention.py:201-234)
+
+
+def test_rejects_empty_sequence() -> None:
+    c = decode_case([3, 5], 4, 2, head_dim=32)
+    c.context_lens[1] = 0
+    with pytest.raises(ValueError, match="at least one token"):
+        hip_attention.paged_decode_attention(*c.args(), c.scale, c.block_size)
+
+
+def test_rejects_non_power_of_two_head_dim() -> None:
+    c = decode_case([3], 4, 2, head_dim=24)
+    with pytest.raises(ValueError, match="power of 2"):
+        hip_attention.paged_decode_attention(*c.args(), c.scale, c.block_size)
+
+
+def test_rejects_int64_block_tables() -> None:
+    c = decode_case([3], 4, 2, head_dim=32)
+    with pytest.raises(ValueError, match="int32"):
+        hip_attention.paged_decode_attention(
+            c.q, c.k_cache, c.v_cache, c.block_tables.long(), c.context_lens, c.scale, 16
+        )
+
+
+def test_rejects_heads_that_do_not_group() -> None:
+    c = decode_case([3], 6, 4, head_dim=32)
+    with pytest.raises(ValueError, match="groups"):
+        hip_attention.paged_decode_attention(*c.args(), c.scale, c.block_size)
+
+
+def test_grouped_kernels_reject_a_group_that_is_not_a_power_of_2() -> None:
+    c = decode_case([3], 12, 4, head_dim=32)
+    for fn in (hip_attention.paged_decode_attention_grouped, hip_attention.paged_decode_attention_split):
+        with pytest.raises(ValueError, match="power-of-2 head group"):
+            fn(*c.args(), c.scale, c.block_size)
+
+
+def test_split_count_out_of_range_is_refused() -> None:  # test_kernel_variants.py:67-71
+    c = decode_case([20], head_dim=32, block_size=4)
+    for bad in (-1, hip_attention.MAX_SPLITS + 1):
+        with pytest.raises(ValueError, match="num_splits"):
+            hip_attention.launch_paged_decode_split(*c.args(), c.scale, c.block_size, num_splits=bad)
+
+
+@pytest.mark.parametrize("tile", [(3, 4), (2, 3), (0, 4)])
+def test_rejects_a_tile_that_is_not_powers_of_2(tile: tuple[int, int]) -> None:
+    c = decode_case([3], 4, 2, head_dim=32, block_size=4)
+    with pytest.raises(ValueError, match="powers of 2"):
+        hip_attention.launch_paged_decode_split(*c.args(), c.scale, c.block_size, 2, tile)
+    with pytest.raises(ValueError, match="powers of 2"):
+        hip_attention.launch_paged_decode_grouped(*c.args(), c.scale, c.block_size, tile)
+
+
+def test_cpu_tensors_are_refused_not_computed() -> None:
+    c = decode_case([3, 9], 4, 2, head_dim=32)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        hip_attention.paged_decode_attention_split(*c.args(), c.scale, c.block_size)
+    p = prefill_case([(0, 5)])
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        hip_prefill.paged_prefill_attention(*p.args())
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        hip_fused.rms_norm_rows(torch.randn(2, 16), torch.randn(16), 1e-6)
+
+
+def test_split_policy_tables() -> None:
+    # The reference's T4 policy, reproduced exactly with its constants
+    # (test_triton_attention.py:240-249) ...
+    t4 = {"target": hip_attention.T4_TARGET_PROGRAMS, "no_split": hip_attention.T4_NO_SPLIT_PROGRAMS}
+    batches = (1, 2, 4, 8, 10, 16, 24, 31, 32, 64)
+    assert [hip_attention.num_splits_for(b, 8, 64, **t4) for b in batches] == [
+        16, 16, 16, 16, 13, 8, 6, 5, 1, 1]  # fmt: skip
+    assert hip_attention.num_splits_for(1, 8, 4, **t4) == 4
+    assert hip_attention.num_splits_for(1, 1, 64, **t4) == hip_attention.MAX_SPLITS
+    assert hip_attention.num_splits_for(256, 1, 64, **t4) == 1
+    # ... and the MI355X default: about 4096 waves, never more than the table width.
+    assert [hip_attention.num_splits_for(b, 8, 256) for b in (1, 8, 32, 64, 128, 512)] == [
+        16, 16, 16, 8, 4, 1]  # fmt: skip
+    assert hip_attention.num_splits_for(64, 8, 4) == 4
+
+
+# --- prefill and fused argument errors (test_triton_prefill.py:173-185,
+#     test_triton_fused.py:53-59, :102-111)
+
+
+def test_prefill_rejects_bad_arguments() -> None:
+    case = prefill_case([(0, 5)])
+    args = case.args()
+    with pytest.raises(ValueError):
+        hip_prefill.paged_prefill_attention(*args, rows_per_tile=8)
+    with pytest.raises(ValueError):
+        hip_prefill.paged_prefill_attention(*args, block_n=24)
+    q3 = case.q[:, :3].contiguous()
+    with pytest.raises(ValueError):
+        hip_prefill.paged_prefill_attention(q3, case.k, case.v, case.tables, case.starts,
+                                            case.q_lens, case.ctx_lens, 1.0, 4, 5)  # fmt: skip
+    with pytest.raises(ValueError):
+        hip_prefill.paged_prefill_attention(case.q, case.k, case.v, case.tables, case.starts.long(),
+                                            case.q_lens, case.ctx_lens, 1.0, 4, 5)  # fmt: skip
+
+
+def test_rms_norm_rows_of_nothing_and_bad_shapes() -> None:
+    assert hip_fused.rms_norm_rows(torch.randn(0, 16), torch.randn(16), 1e-6).shape == (0, 16)
+    with pytest.raises(ValueError):
+        hip_fused.rms_norm_rows(torch.randn(2, 3, 16), torch.randn(16), 1e-6)
+    with pytest.raises(ValueError):
+        hip_fused.rms_norm_rows(torch.randn(2, 16), torch.randn(8), 1e-6)
+
+
+def test_qk_norm_rope_store_rejects_bad_shapes() -> None:
+    t, hq, hkv, d = 3, 4, 2, 8
+    q, k, v = torch.randn(t, hq, d), torch.randn(t, hkv, d), torch.randn(t, hkv, d)
+    w = torch.randn(d)
+    cos = sin = torch.randn(t, d)
+    slots = torch.arange(t)
+    kc = vc = torch.randn(16, hkv, d)
+    with pytest.raises(ValueError):  # v with the wrong number of heads
+        hip_fused.qk_norm_rope_store(q, k, q, w, w, cos, sin, slots, kc, vc, 1e-6)
+    with pytest.raises(ValueError):  # tables for the wrong number of tokens
+        hip_fused.qk_norm_rope_store(q, k, v, w, w, cos[:2], sin[:2], slots, kc, vc, 1e-6)

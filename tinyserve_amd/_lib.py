@@ -1,0 +1,119 @@
+"""ctypes binding of ``libtinyserve_amd.so`` (the C ABI in ``include/tinyserve_amd.h``).
+
+``torch`` is imported first on purpose: it loads the HIP runtime it ships
+(``libamdhip64.so.7``), and the library then binds to that same runtime instead of a
+second copy, so both share one device context, one allocator and torch's streams.
+
+There is no fallback: if the library is missing, or a tensor is not on a HIP device,
+the entry points raise instead of computing anything on the CPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libtinyserve_amd.so")
+
+_c_i32p = ctypes.POINTER(ctypes.c_int32)
+_c_i64p = ctypes.POINTER(ctypes.c_int64)
+_vp, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+
+# Every exported function and its argument types, in header order.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "ts_version": (_i, []),
+    "ts_strerror": (ctypes.c_char_p, [_i]),
+    "ts_decode_split": (
+        _i,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,  # q k v bt lens out m l acc
+         _i, _i, _i, _i, _i,  # B Hq Hkv D block_size
+         _i64, _i64, _i64, _i64, _i64, _i64, _i64,  # strides
+         _i, _i, _f, _i, _vp],  # splits head_tile scale dtype stream
+    ),
+    "ts_decode_combine": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i64, _i, _i, _vp]),
+    "ts_prefill_varlen": (
+        _i,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,  # q k v out bt q_starts q_lens ctx_lens
+         _i, _i, _i, _i, _i, _i,  # R Hq Hkv D block_size max_q_len
+         _i64, _i64, _i64, _i64, _i64, _i64, _i64,  # strides
+         _f, _i, _vp],
+    ),
+    "ts_rms_norm_rows": (_i, [_vp, _vp, _vp, _i, _i, _i64, _i64, _f, _i, _vp]),
+    "ts_qk_norm_rope_store": (
+        _i,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,  # tensors
+         _i, _i, _i, _i,  # T Hq Hkv D
+         *([_i64] * 11),  # strides
+         _f, _i, _i, _vp],
+    ),
+}  # fmt: skip
+
+EXPORTS = tuple(SIGNATURES)
+
+DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library (raises RuntimeError if it has not been built)."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH.name} is not built: run `python -m tinyserve_amd.build` "
+                    "(the HIP kernels have no CPU fallback)"
+                )
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def call(name: str, *args: object) -> None:
+    """Call entry point ``name``; raise on a non-zero status."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.ts_strerror(rc).decode()
+        if rc < 0:
+            raise ValueError(f"{name}: {msg}")
+        raise RuntimeError(f"{name}: HIP error {rc}: {msg}")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return DTYPES[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}: float32, float16 or bfloat16") from None
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """The common HIP device of ``tensors``; RuntimeError for CPU tensors (no fallback)."""
+    dev = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "tinyserve_amd kernels run on a HIP device only (no CPU fallback); "
+                f"got a tensor on {t.device}"
+            )
+        if t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def stream_of(dev: torch.device) -> int:
+    """Handle of torch's current stream on ``dev`` (the kernels launch there)."""
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,446 @@
+// Paged GQA decode attention for gfx950: one wave64 per (sequence, query-head tile,
+// split), the split-K combine pass, and the same loop reused as the generic (fp32 /
+// small head_dim) varlen prefill path.
+//
+// Reference behaviour: src/tinyserve/triton_attention.py:76-327 (per-head, grouped and
+// split kernels, merge kernel), numerics of src/tinyserve/attention.py:62-141.
+//
+// Lane layout. A head row of D elements is read by LPT consecutive lanes ("lanes per
+// token"), each holding E = D / LPT elements as 16-byte vectors; vector i of lane c
+// covers elements (i * LPT + c) * VEC .. + VEC - 1, so one load instruction of the LPT
+// lanes of a token reads LPT * 16 contiguous bytes. A wave therefore streams
+// TPW = 64 / LPT tokens per iteration (16 tokens of a 16-slot block for fp16 D=128:
+// 4 KB of K and 4 KB of V per wave per iteration, both issued before the previous
+// iteration's math so that two iterations are always in flight).
+//
+// Softmax. Every token lane keeps its own running (max, sum, acc) per query head (the
+// online softmax of triton_attention.py:14-22, in base 2), so the loop has no
+// cross-lane work except the LPT-lane dot-product reduction. The token lanes are
+// merged once at the end with the two-partial rule m = max(m1, m2),
+// l = 2^(m1-m) l1 + 2^(m2-m) l2 (same for acc), the rule the combine pass uses too.
+#include "common.h"
+
+namespace ts {
+
+template <typename T, int D>
+struct RowShape {
+  static constexpr int kRowBytes = D * static_cast<int>(sizeof(T));
+  static constexpr int kLPT = kRowBytes <= 64 ? 1 : (kRowBytes / 64 > 64 ? 64 : kRowBytes / 64);
+  static constexpr int kE = D / kLPT;
+  static constexpr int kVec = 16 / static_cast<int>(sizeof(T));
+  static constexpr int kNV = kE / kVec;
+  static constexpr int kTPW = kWave / kLPT;
+  static_assert(kNV >= 1 && kNV * kVec == kE, "a head row must be a multiple of 16 bytes");
+};
+
+struct AttendArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* bt;
+  const int32_t* lens;  // decode: context_lens; prefill: context_lens of each sequence
+  void* out;
+  float* m;
+  float* l;
+  float* acc;
+  const int32_t* q_starts;  // prefill only
+  const int32_t* q_lens;    // prefill only
+  int Hq;
+  int group;  // query heads per kv head
+  int lbs;    // log2(block_size)
+  int splits;
+  int max_q_len;  // prefill only
+  int64_t q_sb, q_sh, o_sb, o_sh, k_ss, k_sh, bt_s;
+  float scale_log2;  // softmax scale * log2(e)
+};
+
+// Partial dot product of one 16-byte K vector with the matching q vector, fp32 result
+// (v_dot2_f32_{f16,bf16}: two products per instruction, fp32 accumulation).
+__device__ __forceinline__ float dot16(const Pack16<f16>& a, const Pack16<f16>& b, float s) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const h2 x = {a.v[2 * j], a.v[2 * j + 1]};
+    const h2 y = {b.v[2 * j], b.v[2 * j + 1]};
+    s = __builtin_amdgcn_fdot2(x, y, s, false);
+  }
+  return s;
+}
+__device__ __forceinline__ float dot16(const Pack16<bf16>& a, const Pack16<bf16>& b, float s) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const b2 x = {a.v[2 * j], a.v[2 * j + 1]};
+    const b2 y = {b.v[2 * j], b.v[2 * j + 1]};
+    s = __builtin_amdgcn_fdot2_f32_bf16(x, y, s, false);
+  }
+  return s;
+}
+__device__ __forceinline__ float dot16(const Pack16<float>& a, const Pack16<float>& b, float s) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s = fmaf(a.v[j], b.v[j], s);
+  return s;
+}
+
+template <typename T, int D, int HT>
+struct TokenState {
+  using S = RowShape<T, D>;
+  float m[HT];
+  float l[HT];
+  float acc[HT][S::kE];
+};
+
+// Merge the partial softmax states of lanes OFF apart (token lanes only: OFF >= LPT).
+template <int OFF, typename T, int D, int HT>
+__device__ __forceinline__ void merge_lanes(TokenState<T, D, HT>& st) {
+  using S = RowShape<T, D>;
+#pragma unroll
+  for (int g = 0; g < HT; ++g) {
+    const float mo = xor_lane<OFF>(st.m[g]);
+    const float lo = xor_lane<OFF>(st.l[g]);
+    const float mn = fmaxf(st.m[g], mo);
+    const float a1 = fast_exp2(st.m[g] - mn);
+    const float a2 = fast_exp2(mo - mn);
+    st.l[g] = st.l[g] * a1 + lo * a2;
+#pragma unroll
+    for (int e = 0; e < S::kE; ++e) st.acc[g][e] = st.acc[g][e] * a1 + xor_lane<OFF>(st.acc[g][e]) * a2;
+    st.m[g] = mn;
+  }
+}
+
+template <typename T, int D, int HT>
+__device__ __forceinline__ void merge_token_lanes(TokenState<T, D, HT>& st) {
+  constexpr int L = RowShape<T, D>::kLPT;
+  if constexpr (L <= 1) merge_lanes<1>(st);
+  if constexpr (L <= 2) merge_lanes<2>(st);
+  if constexpr (L <= 4) merge_lanes<4>(st);
+  if constexpr (L <= 8) merge_lanes<8>(st);
+  if constexpr (L <= 16) merge_lanes<16>(st);
+  if constexpr (L <= 32) merge_lanes<32>(st);
+}
+
+// A finite "no score yet" maximum: 2^(kNoMax - real score) is exactly 0, and two empty
+// states merge to an empty state without inf - inf.
+constexpr float kNoMax = -1.0e30f;
+
+template <typename T, int D, int HT, bool PREFILL>
+__global__ __launch_bounds__(64) void paged_attend_kernel(const AttendArgs a) {
+  using S = RowShape<T, D>;
+  constexpr int LPT = S::kLPT, NV = S::kNV, VEC = S::kVec, TPW = S::kTPW, E = S::kE;
+  const int lane = threadIdx.x;
+  const int c = lane % LPT;
+  const int tl = lane / LPT;
+  const int h0 = blockIdx.y * HT;
+  const int kvh = h0 / a.group;
+
+  int seq, ctx, split = 0;
+  int64_t qrow, orow;
+  if constexpr (PREFILL) {
+    seq = blockIdx.x / a.max_q_len;
+    const int i = blockIdx.x - seq * a.max_q_len;
+    const int ql = a.q_lens[seq];
+    if (i >= ql) return;  // the grid covers the longest sequence
+    const int row = a.q_starts[seq] + i;
+    ctx = a.lens[seq] - ql + i + 1;  // causal: keys 0 .. its own position
+    qrow = row * a.q_sb;
+    orow = row * a.o_sb;
+  } else {
+    seq = blockIdx.x;
+    split = blockIdx.z;
+    ctx = a.lens[seq];
+    qrow = seq * a.q_sb;
+    orow = seq * a.o_sb;
+  }
+  const int lbs = a.lbs;
+  const int bs_mask = (1 << lbs) - 1;
+  const int nblocks = (ctx + bs_mask) >> lbs;
+  const int per = (nblocks + a.splits - 1) / a.splits;
+  const int first = split * per;
+  const int last = min(first + per, nblocks);
+
+  const T* qp = static_cast<const T*>(a.q) + qrow;
+  Pack16<T> qv[HT][NV];
+#pragma unroll
+  for (int g = 0; g < HT; ++g)
+#pragma unroll
+    for (int i = 0; i < NV; ++i) qv[g][i] = load16(qp + (h0 + g) * a.q_sh + (i * LPT + c) * VEC);
+
+  TokenState<T, D, HT> st;
+#pragma unroll
+  for (int g = 0; g < HT; ++g) {
+    st.m[g] = kNoMax;
+    st.l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) st.acc[g][e] = 0.f;
+  }
+
+  if (first < last) {
+    const int t0 = first << lbs;
+    const int t1 = min(last << lbs, ctx);
+    const int32_t* btrow = a.bt + seq * a.bt_s;
+    const T* kbase = static_cast<const T*>(a.k) + kvh * a.k_sh + c * VEC;
+    const T* vbase = static_cast<const T*>(a.v) + kvh * a.k_sh + c * VEC;
+    // Lane j holds block-table entry `chunk + j`: a window of 64 blocks, refreshed when
+    // the positions pass its end. An iteration never straddles two windows (it covers
+    // TPW <= 64 positions starting at a multiple of TPW from a window start).
+    int chunk = first;
+    int win = (chunk + lane < last) ? btrow[chunk + lane] : 0;
+
+    Pack16<T> kc[NV], vc[NV], kn[NV], vn[NV];
+    auto issue = [&](Pack16<T>(&kf)[NV], Pack16<T>(&vf)[NV], int p0) {
+      if (((p0 >> lbs) - chunk) >= 64) {
+        chunk += 64;
+        win = (chunk + lane < last) ? btrow[chunk + lane] : 0;
+      }
+      const int pos = p0 + tl;
+      // A lane past the range reads the range's first token (owned and finite) and
+      // is masked out of the softmax below.
+      const int pe = pos < t1 ? pos : p0;
+      const int blk = __shfl(win, (pe >> lbs) - chunk);
+      const int64_t off = ((static_cast<int64_t>(blk) << lbs) + (pe & bs_mask)) * a.k_ss;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        kf[i] = load16(kbase + off + i * LPT * VEC);
+        vf[i] = load16(vbase + off + i * LPT * VEC);
+      }
+    };
+
+    auto attend = [&](const Pack16<T>(&kf)[NV], const Pack16<T>(&vf)[NV], int p0) {
+      const bool valid = p0 + tl < t1;
+      float s[HT];
+      bool grow = false;
+#pragma unroll
+      for (int g = 0; g < HT; ++g) {
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) d = dot16(kf[i], qv[g][i], d);
+        d = group_sum<LPT>(d) * a.scale_log2;
+        s[g] = valid ? d : -INFINITY;
+        grow |= s[g] > st.m[g];
+      }
+      float vf32[E];
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) vf32[i * VEC + j] = to_f32(vf[i].v[j]);
+      if (__any(grow)) {
+#pragma unroll
+        for (int g = 0; g < HT; ++g) {
+          const float mn = fmaxf(st.m[g], s[g]);
+          const float al = fast_exp2(st.m[g] - mn);
+          const float p = fast_exp2(s[g] - mn);
+          st.l[g] = st.l[g] * al + p;
+#pragma unroll
+          for (int e = 0; e < E; ++e) st.acc[g][e] = fmaf(p, vf32[e], st.acc[g][e] * al);
+          st.m[g] = mn;
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < HT; ++g) {
+          const float p = fast_exp2(s[g] - st.m[g]);
+          st.l[g] += p;
+#pragma unroll
+          for (int e = 0; e < E; ++e) st.acc[g][e] = fmaf(p, vf32[e], st.acc[g][e]);
+        }
+      }
+    };
+
+    // Two iterations in flight: the next one's loads are issued before this one's math.
+    int p0 = t0;
+    issue(kc, vc, p0);
+    while (true) {
+      const int p1 = p0 + TPW;
+      if (p1 < t1) issue(kn, vn, p1);
+      attend(kc, vc, p0);
+      if (p1 >= t1) break;
+      const int p2 = p1 + TPW;
+      if (p2 < t1) issue(kc, vc, p2);
+      attend(kn, vn, p1);
+      if (p2 >= t1) break;
+      p0 = p2;
+    }
+  }
+
+  merge_token_lanes(st);
+  if (tl != 0) return;
+
+  if (PREFILL || a.splits == 1) {
+    T* op = static_cast<T*>(a.out) + orow;
+#pragma unroll
+    for (int g = 0; g < HT; ++g) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        Pack16<T> o;
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) o.v[j] = from_f32<T>(st.acc[g][i * VEC + j] / st.l[g]);
+        store16(op + (h0 + g) * a.o_sh + (i * LPT + c) * VEC, o);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < HT; ++g) {
+      const int64_t part = (static_cast<int64_t>(seq) * a.Hq + h0 + g) * a.splits + split;
+      if (c == 0) {
+        a.m[part] = st.l[g] > 0.f ? st.m[g] : -INFINITY;
+        a.l[part] = st.l[g];
+      }
+      float* ap = a.acc + part * D;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int j = 0; j < VEC; j += 4)
+          *reinterpret_cast<float4*>(ap + (i * LPT + c) * VEC + j) =
+              make_float4(st.acc[g][i * VEC + j], st.acc[g][i * VEC + j + 1],
+                          st.acc[g][i * VEC + j + 2], st.acc[g][i * VEC + j + 3]);
+    }
+  }
+}
+
+// The split-K combine: one wave per (sequence, query head).
+template <typename T>
+__global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ m,
+                                                     const float* __restrict__ l,
+                                                     const float* __restrict__ acc, T* out,
+                                                     int Hq, int D, int64_t o_sb, int64_t o_sh,
+                                                     int splits) {
+  const int b = blockIdx.x, h = blockIdx.y;
+  const int64_t base = (static_cast<int64_t>(b) * Hq + h) * splits;
+  float mmax = -INFINITY;
+  for (int s = 0; s < splits; ++s) mmax = fmaxf(mmax, m[base + s]);
+  float den = 0.f;
+  for (int s = 0; s < splits; ++s) den += fast_exp2(m[base + s] - mmax) * l[base + s];
+  T* op = out + b * o_sb + h * o_sh;
+  for (int d = threadIdx.x; d < D; d += kWave) {
+    float num = 0.f;
+    for (int s = 0; s < splits; ++s) num += fast_exp2(m[base + s] - mmax) * acc[(base + s) * D + d];
+    op[d] = from_f32<T>(num / den);
+  }
+}
+
+template <typename T, int D, int HT, bool PREFILL>
+static int launch_attend(const AttendArgs& a, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, PREFILL>), grid, dim3(kWave), 0, stream, a);
+  return launch_status();
+}
+
+template <typename T, bool PREFILL>
+static int dispatch_d(const AttendArgs& a, int D, int ht, dim3 grid, hipStream_t stream) {
+#define TS_HT(DD)                                                           \
+  switch (ht) {                                                             \
+    case 1: return launch_attend<T, DD, 1, PREFILL>(a, grid, stream);       \
+    case 2: return launch_attend<T, DD, 2, PREFILL>(a, grid, stream);       \
+    case 4: return launch_attend<T, DD, 4, PREFILL>(a, grid, stream);       \
+    default: return TS_EUNSUPPORTED;                                        \
+  }
+  switch (D) {
+    case 8: TS_HT(8)
+    case 16: TS_HT(16)
+    case 32: TS_HT(32)
+    case 64: TS_HT(64)
+    case 128: TS_HT(128)
+    case 256: TS_HT(256)
+    default: break;
+  }
+#undef TS_HT
+  return TS_EUNSUPPORTED;
+}
+
+template <bool PREFILL>
+static int dispatch_attend(const AttendArgs& a, int dtype, int D, int ht, dim3 grid,
+                           hipStream_t stream) {
+  switch (dtype) {
+    case TS_F32: return dispatch_d<float, PREFILL>(a, D, ht, grid, stream);
+    case TS_F16: return dispatch_d<f16, PREFILL>(a, D, ht, grid, stream);
+    case TS_BF16: return dispatch_d<bf16, PREFILL>(a, D, ht, grid, stream);
+    default: return TS_EUNSUPPORTED;
+  }
+}
+
+// Query heads one wave handles: 1 (per-head launch) or the GQA group, at most 4 (larger
+// groups use several waves per kv head, each re-reading the kv head's blocks).
+static int head_tile_for(int group, int head_tile) {
+  if (head_tile == 1) return 1;
+  if (head_tile != 0 || !is_pow2(group)) return -1;
+  return group < 4 ? group : 4;
+}
+
+// The generic varlen prefill (fp32 or head dims without an MFMA kernel): one wave per
+// (query row, head tile) running the decode loop over keys 0 .. its position.
+int prefill_rows_generic(const void* q, const void* k, const void* v, void* out,
+                         const int32_t* bt, const int32_t* q_starts, const int32_t* q_lens,
+                         const int32_t* ctx_lens, int R, int Hq, int Hkv, int D, int lbs,
+                         int max_q_len, int64_t q_st, int64_t q_sh, int64_t o_st, int64_t o_sh,
+                         int64_t k_ss, int64_t k_sh, int64_t bt_s, float scale, int dtype,
+                         hipStream_t stream) {
+  const int group = Hq / Hkv;
+  const int ht = head_tile_for(group, 0);
+  if (ht < 0) return TS_EINVAL;
+  AttendArgs a{q, k, v, bt, ctx_lens, out, nullptr, nullptr, nullptr, q_starts, q_lens,
+               Hq, group, lbs, 1, max_q_len, q_st, q_sh, o_st, o_sh, k_ss, k_sh, bt_s,
+               scale * kLog2e};
+  dim3 grid(static_cast<unsigned>(R) * max_q_len, Hq / ht, 1);
+  return dispatch_attend<true>(a, dtype, D, ht, grid, stream);
+}
+
+}  // namespace ts
+
+using namespace ts;
+
+extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v_cache,
+                               const int32_t* block_tables, const int32_t* context_lens,
+                               void* out, float* m, float* l, float* acc, int B, int Hq,
+                               int Hkv, int D, int block_size, int64_t q_stride_b,
+                               int64_t q_stride_h, int64_t o_stride_b, int64_t o_stride_h,
+                               int64_t k_stride_slot, int64_t k_stride_head, int64_t bt_stride,
+                               int splits, int head_tile, float scale, int dtype,
+                               void* stream) {
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || splits < 1 || !is_pow2(block_size))
+    return TS_EINVAL;
+  if (B == 0) return 0;
+  if (splits > 1 && (!m || !l || !acc)) return TS_EINVAL;
+  if (splits == 1 && !out) return TS_EINVAL;
+  const int group = Hq / Hkv;
+  const int ht = head_tile_for(group, head_tile);
+  if (ht < 0) return TS_EINVAL;
+  AttendArgs a{q, k_cache, v_cache, block_tables, context_lens, out, m, l, acc, nullptr,
+               nullptr, Hq, group, ilog2(block_size), splits, 0, q_stride_b, q_stride_h,
+               o_stride_b, o_stride_h, k_stride_slot, k_stride_head, bt_stride,
+               scale * kLog2e};
+  dim3 grid(B, Hq / ht, splits);
+  return dispatch_attend<false>(a, dtype, D, ht, grid, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ts_decode_combine(const float* m, const float* l, const float* acc, void* out,
+                                 int B, int Hq, int D, int64_t o_stride_b, int64_t o_stride_h,
+                                 int splits, int dtype, void* stream) {
+  if (B < 0 || Hq <= 0 || D <= 0 || splits < 1) return TS_EINVAL;
+  if (B == 0) return 0;
+  dim3 grid(B, Hq);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case TS_F32:
+      hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(kWave), 0, st, m, l, acc,
+                         static_cast<float*>(out), Hq, D, o_stride_b, o_stride_h, splits);
+      break;
+    case TS_F16:
+      hipLaunchKernelGGL(combine_kernel<f16>, grid, dim3(kWave), 0, st, m, l, acc,
+                         static_cast<f16*>(out), Hq, D, o_stride_b, o_stride_h, splits);
+      break;
+    case TS_BF16:
+      hipLaunchKernelGGL(combine_kernel<bf16>, grid, dim3(kWave), 0, st, m, l, acc,
+                         static_cast<bf16*>(out), Hq, D, o_stride_b, o_stride_h, splits);
+      break;
+    default: return TS_EUNSUPPORTED;
+  }
+  return launch_status();
+}
+
+extern "C" int ts_version(void) { return (0 << 16) | 1; }
+
+extern "C" const char* ts_strerror(int code) {
+  if (code == 0) return "success";
+  if (code == TS_EINVAL) return "invalid argument: sizes or strides do not fit together";
+  if (code == TS_EUNSUPPORTED) return "unsupported shape or dtype: no compiled kernel";
+  if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+  return "unknown error";
+}

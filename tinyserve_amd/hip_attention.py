@@ -1,0 +1,272 @@
+"""Paged decode attention on MI355X: the entry points of the reference's
+``tinyserve.triton_attention`` (src/tinyserve/triton_attention.py:330-586), same names,
+arguments, results and errors, launching the HIP kernels of ``csrc/decode.hip``.
+
+Kernel shape (gfx950). One wave64 per (sequence, query-head tile, split): the grouped
+and split launches give a wave the whole GQA group of one kv head (both query heads of
+Qwen3-0.6B), so every K/V byte is read once; the per-query-head launch
+(``paged_decode_attention``, any head grouping) gives it one query head. Each wave
+streams 16-byte K/V vectors of its range of cache blocks, two iterations in flight, and
+keeps an online softmax per token lane, merged across lanes once at the end. With more
+than one split, every range writes an fp32 partial (m, l, acc) and a second kernel
+combines them (the reference's ``_merge_splits_kernel``, :299-327).
+
+Every launch goes on torch's current stream, never synchronises and never allocates
+outside torch's caching allocator, so a HIP graph can capture the ``launch_*``
+functions. ``check_decode_args`` reads ``context_lens`` back (a host sync), as the
+reference's does (:361-391).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from tinyserve_amd import _lib
+
+# The reference's names for its tuning knobs. ``NO_SPECIALIZE`` and ``DECODE_TILE`` are
+# Triton launch options there (:62, :73); the HIP kernels have one compiled variant per
+# (dtype, head_dim, heads per wave) whatever the batch looks like, and choose their own
+# tiling, so a ``tile`` argument is validated (``check_tile``) and otherwise unused.
+NO_SPECIALIZE = ["stride_bt", "num_splits"]
+DECODE_TILE = (1, 1)
+
+# Split-K policy (the reference's :488-510, retuned for 256 CUs). A wave needs several
+# hundred KB of K/V in flight per CU to approach the HBM roofline, so the launch aims at
+# TARGET_PROGRAMS waves and stops splitting once the batch alone gives
+# NO_SPLIT_PROGRAMS. The reference's T4 values were 1024 and 256.
+TARGET_PROGRAMS = 4096
+NO_SPLIT_PROGRAMS = 4096
+MAX_SPLITS = 16
+
+# Reference constants, kept for ``num_splits_for(..., target=..., no_split=...)`` callers
+# that want the T4 policy exactly.
+T4_TARGET_PROGRAMS = 1024
+T4_NO_SPLIT_PROGRAMS = 256
+
+
+def check_decode_args(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    block_size: int,
+) -> None:
+    """Raise ValueError if the arguments do not fit together (triton_attention.py:361-391).
+
+    The last check reads ``context_lens`` to the host (a sync), so it is separate from
+    the ``launch_*`` functions, which a graph can capture."""
+    b, num_q_heads, head_dim = q.shape
+    num_kv_heads = k_cache.shape[1]
+    if num_q_heads % num_kv_heads:
+        raise ValueError(f"{num_q_heads} query heads do not split into {num_kv_heads} groups")
+    for name, n in (("head_dim", head_dim), ("block_size", block_size)):
+        if n < 1 or n & (n - 1):
+            raise ValueError(f"{name} must be a power of 2, got {n}")
+    if k_cache.shape != v_cache.shape or k_cache.shape[2] != head_dim:
+        raise ValueError(f"cache shapes {k_cache.shape} / {v_cache.shape} vs q {q.shape}")
+    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
+        raise ValueError("block_tables and context_lens must be int32")
+    if context_lens.shape != (b,) or block_tables.shape[0] != b:
+        raise ValueError(f"need one block-table row and one length per sequence ({b})")
+    if q.stride(2) != 1 or k_cache.stride(2) != 1 or v_cache.stride() != k_cache.stride():
+        raise ValueError("the head dimension must be contiguous, and k/v laid out alike")
+    _check_kernel_shape(q, k_cache)
+    if bool((context_lens < 1).any()):
+        raise ValueError("every sequence needs at least one token")
+
+
+def _check_kernel_shape(q: torch.Tensor, k_cache: torch.Tensor) -> None:
+    """Shapes the compiled kernels cover (head rows of 16 bytes .. 256 elements)."""
+    head_dim = q.shape[2]
+    if q.dtype != k_cache.dtype:
+        raise ValueError(f"q is {q.dtype} but the cache is {k_cache.dtype}")
+    if q.dtype not in _lib.DTYPES:
+        raise ValueError(f"unsupported dtype {q.dtype}")
+    if head_dim * q.element_size() < 16 or head_dim > 256:
+        raise ValueError(f"head_dim {head_dim} is outside the HIP kernels' range (8..256)")
+
+
+def check_tile(tile: tuple[int, int]) -> tuple[int, int]:
+    """``tile`` if both numbers are powers of 2 (the reference's check, :480-485)."""
+    blocks, warps = tile
+    if blocks < 1 or blocks & (blocks - 1) or warps < 1 or warps & (warps - 1):
+        raise ValueError(f"tile blocks and warps must be powers of 2, got {tile}")
+    return tile
+
+
+def num_splits_for(
+    batch: int,
+    num_kv_heads: int,
+    max_blocks: int,
+    target: int | None = None,
+    no_split: int | None = None,
+) -> int:
+    """Ranges to split each sequence's blocks into (triton_attention.py:499-510): enough
+    for about ``target`` waves, at most ``MAX_SPLITS`` and the block-table width; 1 once
+    the batch alone gives ``no_split`` waves. Depends only on shapes, never on lengths,
+    so a captured graph always launches the same grid."""
+    target = TARGET_PROGRAMS if target is None else target
+    no_split = NO_SPLIT_PROGRAMS if no_split is None else no_split
+    programs = batch * num_kv_heads
+    if programs >= no_split:
+        return 1
+    want = -(-target // programs)
+    return max(1, min(want, MAX_SPLITS, max_blocks))
+
+
+def _launch(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+    splits: int,
+    head_tile: int,
+) -> torch.Tensor:
+    dev = _lib.require_device(q, k_cache, v_cache, block_tables, context_lens)
+    _check_kernel_shape(q, k_cache)
+    b, hq, d = q.shape
+    hkv = k_cache.shape[1]
+    out = torch.empty_like(q)
+    if b == 0:
+        return out
+    stream = _lib.stream_of(dev)
+    dt = _lib.dtype_code(q)
+    strides = (q.stride(0), q.stride(1), out.stride(0), out.stride(1),
+               k_cache.stride(0), k_cache.stride(1), block_tables.stride(0))  # fmt: skip
+    if splits == 1:
+        _lib.call("ts_decode_split", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                  block_tables.data_ptr(), context_lens.data_ptr(), out.data_ptr(),
+                  None, None, None, b, hq, hkv, d, block_size, *strides, 1, head_tile,
+                  scale, dt, stream)  # fmt: skip
+        return out
+    m = torch.empty((b, hq, splits), dtype=torch.float32, device=dev)
+    l = torch.empty_like(m)  # noqa: E741
+    acc = torch.empty((b, hq, splits, d), dtype=torch.float32, device=dev)
+    _lib.call("ts_decode_split", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+              block_tables.data_ptr(), context_lens.data_ptr(), out.data_ptr(),
+              m.data_ptr(), l.data_ptr(), acc.data_ptr(), b, hq, hkv, d, block_size,
+              *strides, splits, head_tile, scale, dt, stream)  # fmt: skip
+    _lib.call("ts_decode_combine", m.data_ptr(), l.data_ptr(), acc.data_ptr(), out.data_ptr(),
+              b, hq, d, out.stride(0), out.stride(1), splits, dt, stream)  # fmt: skip
+    return out
+
+
+def paged_decode_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+) -> torch.Tensor:
+    """Decode attention for B sequences in one launch (triton_attention.py:330-358).
+
+    Args:
+        q: ``[B, Hq, D]``, each sequence's one new query, RoPE-rotated.
+        k_cache, v_cache: ``[num_slots, Hkv, D]``, one layer of the cache, the new
+            tokens' k/v already written.
+        block_tables: ``[B, max_blocks]`` int32, each sequence's blocks in order.
+        context_lens: ``[B]`` int32, tokens per sequence including the new one (>= 1).
+        scale: multiplies the scores.
+        block_size: tokens per cache block.
+
+    Returns:
+        ``[B, Hq, D]`` in q's dtype.
+    """
+    check_decode_args(q, k_cache, v_cache, block_tables, context_lens, block_size)
+    return launch_paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, block_size)
+
+
+def launch_paged_decode(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+) -> torch.Tensor:
+    """The per-query-head launch alone (:394-421): no checks, no host sync."""
+    return _launch(q, k_cache, v_cache, block_tables, context_lens, scale, block_size, 1, 1)
+
+
+def paged_decode_attention_grouped(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+) -> torch.Tensor:
+    """``paged_decode_attention`` with one wave per (sequence, kv head) (:424-444); needs
+    ``Hq / Hkv`` to be a power of 2."""
+    check_decode_args(q, k_cache, v_cache, block_tables, context_lens, block_size)
+    group = q.shape[1] // k_cache.shape[1]
+    if group & (group - 1):
+        raise ValueError(f"the grouped kernel needs a power-of-2 head group, got {group}")
+    return launch_paged_decode_grouped(
+        q, k_cache, v_cache, block_tables, context_lens, scale, block_size
+    )
+
+
+def launch_paged_decode_grouped(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+    tile: tuple[int, int] | None = None,
+) -> torch.Tensor:
+    """The grouped launch alone (:447-477): no checks, no host sync."""
+    check_tile(tile or DECODE_TILE)
+    return _launch(q, k_cache, v_cache, block_tables, context_lens, scale, block_size, 1, 0)
+
+
+def paged_decode_attention_split(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+) -> torch.Tensor:
+    """The grouped kernel with split-K (:513-531), splits from ``num_splits_for``."""
+    check_decode_args(q, k_cache, v_cache, block_tables, context_lens, block_size)
+    group = q.shape[1] // k_cache.shape[1]
+    if group & (group - 1):
+        raise ValueError(f"the grouped kernel needs a power-of-2 head group, got {group}")
+    return launch_paged_decode_split(
+        q, k_cache, v_cache, block_tables, context_lens, scale, block_size
+    )
+
+
+def launch_paged_decode_split(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+    num_splits: int | None = None,
+    tile: tuple[int, int] | None = None,
+) -> torch.Tensor:
+    """The split-K launches alone (:534-586): no checks, no host sync.
+
+    ``num_splits`` defaults to ``num_splits_for(B, Hkv, max_blocks)``; 1 is the grouped
+    kernel itself, more adds the combine pass."""
+    b = q.shape[0]
+    splits = num_splits or num_splits_for(b, k_cache.shape[1], block_tables.shape[1])
+    if not 1 <= splits <= MAX_SPLITS:
+        raise ValueError(f"num_splits must be 1..{MAX_SPLITS}, got {splits}")
+    check_tile(tile or DECODE_TILE)
+    return _launch(q, k_cache, v_cache, block_tables, context_lens, scale, block_size, splits, 0)

@@ -1,0 +1,106 @@
+"""Fused per-layer kernels around attention on MI355X: ``rms_norm_rows`` and
+``qk_norm_rope_store`` of the reference's ``tinyserve.triton_fused``
+(src/tinyserve/triton_fused.py:116-177), same arguments, results and errors, launching
+``csrc/fused.hip``.
+
+``rms_norm_rows``: one wave64 per row, the row held in registers as 16-byte vectors,
+one HBM read and one write per element.
+
+``qk_norm_rope_store``: one lane group per (token, head); each lane holds a pair of
+16-byte chunks i and i + D/2, so the rotate-half pairs never leave the lane and the
+per-head norm is a reduction over 8 lanes (D = 128, fp16). Query heads go to the
+returned tensor; key heads and value heads are written straight into their cache slots
+(``k_cache[slots[t]]``, ``v_cache[slots[t]]``). Numerics follow layers.py:14-91 step by
+step: fp32 sum of squares, ``1 / sqrt`` (correctly rounded), round to the input dtype,
+multiply by the weight in the input dtype, rotate in fp32 without fused multiply-adds
+(``a*cos - b*sin`` as two rounded products and a difference, like PyTorch), round once.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from tinyserve_amd import _lib
+
+
+def rms_norm_rows(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """``layers.rms_norm`` of every row of ``[T, N]`` in one launch (:116-126)."""
+    if x.dim() != 2 or x.stride(1) != 1 or weight.shape != (x.shape[1],):
+        raise ValueError(f"need a row-contiguous [T, N] tensor and an [N] weight: {x.shape}")
+    if weight.dtype != x.dtype or weight.stride(0) != 1:
+        raise ValueError(f"the weight must be a contiguous {x.dtype} vector, got {weight.dtype}")
+    out = torch.empty_like(x)
+    if x.shape[0]:
+        dev = _lib.require_device(x, weight)
+        _lib.call("ts_rms_norm_rows", x.data_ptr(), weight.data_ptr(), out.data_ptr(),
+                  x.shape[0], x.shape[1], x.stride(0), out.stride(0), float(eps),
+                  _lib.dtype_code(x), _lib.stream_of(dev))  # fmt: skip
+    return out
+
+
+def qk_norm_rope_store(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    slots: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    eps: float,
+) -> torch.Tensor:
+    """q/k head norms, RoPE and the cache write of one layer, in one launch (:129-177).
+
+    Returns ``apply_rope(rms_norm(q, q_weight, eps), cos, sin)`` and writes
+    ``apply_rope(rms_norm(k, k_weight, eps), cos, sin)`` and ``v`` to
+    ``k_cache[slots]`` / ``v_cache[slots]`` (cast to the cache dtype). No host sync.
+
+    Args:
+        q: ``[T, Hq, D]``; k, v: ``[T, Hkv, D]``, head dimension contiguous (strided
+            views of a fused QKV projection are fine).
+        q_weight, k_weight: ``[D]``, q's dtype.
+        cos, sin: ``[T, D]`` float32 from ``rope_cos_sin`` (columns 0 .. D/2-1 are read).
+        slots: ``[T]`` int64 cache slots (int32 is widened).
+        k_cache, v_cache: ``[num_slots, Hkv, D]``, one layer.
+    """
+    t, num_q_heads, head_dim = q.shape
+    num_kv_heads = k.shape[1]
+    if head_dim % 2 or (head_dim // 2) & (head_dim // 2 - 1):
+        raise ValueError(f"head_dim must be twice a power of 2, got {head_dim}")
+    if k.shape != v.shape or k.shape[0] != t or k_cache.shape[1:] != k.shape[1:]:
+        raise ValueError(f"shapes q {q.shape}, k {k.shape}, v {v.shape}, cache {k_cache.shape}")
+    if any(x.stride(2) != 1 for x in (q, k, v, k_cache)) or v_cache.stride() != k_cache.stride():
+        raise ValueError("the head dimension must be contiguous, and k/v caches laid out alike")
+    if cos.shape != (t, head_dim) or cos.stride() != sin.stride() or cos.stride(1) != 1:
+        raise ValueError(f"cos and sin must be [T, D] = {(t, head_dim)}, laid out alike")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        raise ValueError("cos and sin must be float32 (rope_cos_sin)")
+    if head_dim < 8 or head_dim > 256:
+        raise ValueError(f"head_dim {head_dim} is outside the HIP kernels' range (8..256)")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"q, k and v must share a dtype: {q.dtype}, {k.dtype}, {v.dtype}")
+    for w in (q_weight, k_weight):
+        if w.shape != (head_dim,) or w.dtype != q.dtype or w.stride(0) != 1:
+            raise ValueError(f"q/k norm weights must be contiguous [{head_dim}] {q.dtype}")
+    if k_cache.dtype != v_cache.dtype:
+        raise ValueError("k_cache and v_cache must share a dtype")
+    if slots.shape != (t,):
+        raise ValueError(f"slots must be [T] = [{t}]")
+    out = torch.empty_like(q)
+    if t:
+        dev = _lib.require_device(q, k, v, q_weight, k_weight, cos, sin, slots, k_cache, v_cache)
+        if slots.dtype != torch.int64:
+            slots = slots.to(torch.int64)
+        _lib.call(
+            "ts_qk_norm_rope_store",
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            q_weight.data_ptr(), k_weight.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+            slots.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+            t, num_q_heads, num_kv_heads, head_dim,
+            q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+            out.stride(0), out.stride(1), cos.stride(0), k_cache.stride(0), k_cache.stride(1),
+            float(eps), _lib.dtype_code(q), _lib.dtype_code(k_cache), _lib.stream_of(dev),
+        )  # fmt: skip
+    return out

@@ -1,0 +1,105 @@
+"""Varlen causal prefill attention on MI355X: ``paged_prefill_attention`` of the
+reference's ``tinyserve.triton_prefill`` (src/tinyserve/triton_prefill.py:128-216), same
+arguments, result and errors, launching ``csrc/prefill.hip``.
+
+fp16 / bf16 with head_dim 64 or 128 run the MFMA kernel: a workgroup of four wave64s
+owns 32 queries x 4 query heads (or 64 x 2, 128 x 1) of one kv head, gathers each
+64-key tile of K and V from the paged cache into LDS once for all of them, computes
+S^T = K.Q^T and O^T += V^T.P^T with v_mfma_f32_32x32x16, and keeps an online softmax in
+fp32; P is rounded to the input dtype before P.V, as the reference kernel does
+(triton_prefill.py:118). fp32 inputs (exact fp32 dots, the reference's "ieee" path) and
+other head dims run the decode kernel's loop, one wave per (query row, kv head).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from tinyserve_amd import _lib
+
+# The reference's Triton tile (rows_per_tile, block_n, num_warps), :47. The arguments are
+# validated as the reference does and otherwise unused: the HIP kernels choose their tiles.
+DEFAULT_TILE = (64, 32, 8)
+
+
+def paged_prefill_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    q_starts: torch.Tensor,
+    q_lens: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+    max_q_len: int,
+    out: torch.Tensor | None = None,
+    rows_per_tile: int | None = None,
+    block_n: int | None = None,
+    num_warps: int | None = None,
+    ieee: bool | None = None,
+) -> torch.Tensor:
+    """Attention for R prefilling sequences in one launch, reading k/v from the cache.
+
+    Sequence r's queries are rows ``q_starts[r] .. q_starts[r] + q_lens[r] - 1`` of ``q``
+    and are its newest positions ``context_lens[r] - q_lens[r] ..``; each attends causally
+    to its own keys through ``block_tables[r]``.
+
+    Args:
+        q: ``[T, Hq, D]`` RoPE-rotated queries; rows of other sequences are ignored.
+        k_cache, v_cache: ``[num_slots, Hkv, D]``, one layer, the new k/v already written.
+        block_tables: ``[R, max_blocks]`` int32.
+        q_starts, q_lens, context_lens: ``[R]`` int32.
+        max_q_len: the largest ``q_lens`` entry, from the host (sizes the grid, no sync).
+        out: ``[T, Hq, D]`` to write into (other rows are left alone); default
+            ``empty_like(q)``.
+        rows_per_tile, block_n, num_warps, ieee: the reference's Triton knobs; checked
+            like the reference (powers of 2, at least 16 rows / keys) and unused.
+
+    Returns:
+        ``out``.
+    """
+    t, num_q_heads, head_dim = q.shape
+    num_kv_heads = k_cache.shape[1]
+    group = num_q_heads // num_kv_heads
+    rows_per_tile = max(DEFAULT_TILE[0], group) if rows_per_tile is None else rows_per_tile
+    block_n = DEFAULT_TILE[1] if block_n is None else block_n
+    if num_q_heads % num_kv_heads or group & (group - 1):
+        raise ValueError(f"need a power-of-2 head group, got {num_q_heads} / {num_kv_heads}")
+    for name, n in (("block_size", block_size), ("rows_per_tile", rows_per_tile),
+                    ("block_n", block_n)):  # fmt: skip
+        if n < 1 or n & (n - 1):
+            raise ValueError(f"{name} must be a power of 2, got {n}")
+    if rows_per_tile < max(16, group) or block_n < 16:
+        raise ValueError("a tile needs at least 16 rows and 16 keys")
+    if k_cache.shape != v_cache.shape or k_cache.shape[2] != head_dim:
+        raise ValueError(f"cache shapes {k_cache.shape} / {v_cache.shape} vs q {q.shape}")
+    if q.stride(2) != 1 or k_cache.stride(2) != 1 or v_cache.stride() != k_cache.stride():
+        raise ValueError("the head dimension must be contiguous, and k/v laid out alike")
+    r = block_tables.shape[0]
+    for name, x in (("q_starts", q_starts), ("q_lens", q_lens), ("context_lens", context_lens)):
+        if x.dtype != torch.int32 or x.shape != (r,):
+            raise ValueError(f"{name} must be int32 with one entry per sequence ({r})")
+    if block_tables.dtype != torch.int32:
+        raise ValueError("block_tables must be int32")
+    if q.dtype != k_cache.dtype or q.dtype not in _lib.DTYPES:
+        raise ValueError(f"q ({q.dtype}) and the cache ({k_cache.dtype}) must share a float dtype")
+    if head_dim & (head_dim - 1) or head_dim * q.element_size() < 16 or head_dim > 256:
+        raise ValueError(f"head_dim {head_dim} is outside the HIP kernels' range (2^k, 8..256)")
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
+        raise ValueError(f"out must be like q {tuple(q.shape)} {q.dtype}")
+    if r == 0 or t == 0:
+        return out
+    dev = _lib.require_device(q, k_cache, v_cache, block_tables, q_starts, q_lens, context_lens, out)
+    _lib.call(
+        "ts_prefill_varlen",
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+        block_tables.data_ptr(), q_starts.data_ptr(), q_lens.data_ptr(), context_lens.data_ptr(),
+        r, num_q_heads, num_kv_heads, head_dim, block_size, int(max_q_len),
+        q.stride(0), q.stride(1), out.stride(0), out.stride(1),
+        k_cache.stride(0), k_cache.stride(1), block_tables.stride(0),
+        float(scale), _lib.dtype_code(q), _lib.stream_of(dev),
+    )  # fmt: skip
+    return out
