@@ -32,6 +32,12 @@ HIPCC_FLAGS = [
 ]  # fmt: skip
 
 
+# Per-source extra flags. prefill.hip: no NaN handling is needed in its softmax (masked
+# scores are -inf, never NaN), and without it fmaxf skips the NaN-quieting v_max that IEEE
+# mode otherwise puts before every max of an MFMA result.
+EXTRA_FLAGS = {"prefill.hip": ["-fno-honor-nans"]}
+
+
 def hipcc() -> str:
     """Path of hipcc: $HIPCC, then PATH, then /opt/rocm/bin."""
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
@@ -46,7 +52,7 @@ def sources() -> list[Path]:
 
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)

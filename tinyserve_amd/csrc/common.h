@@ -76,6 +76,18 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// Max / sum of x over lanes l and l ^ 32 (the two 32-lane halves), via gfx950's
+// v_permlane32_swap: with both operands x, one result holds x of this lane and the other
+// x of the partner lane (in either order per half), so max/sum of the pair is the answer.
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 inline int ilog2(int x) {

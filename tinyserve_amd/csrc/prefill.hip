@@ -72,24 +72,36 @@ constexpr int kThreads = 256;  // 4 waves
 
 template <typename T, int D>
 struct PrefillShape {
-  static constexpr int kCH = D / 8;                    // 16-byte parts of a row
-  static constexpr int kKPT = kBN * kCH / kThreads;    // keys staged per thread
-  static constexpr int kKStride = D + 8;               // K row stride in LDS (elements)
-  static constexpr int kKBytes = kBN * kKStride * 2;
-  static constexpr int kVBytes = D * kBN * 2;
-  static_assert(kKPT >= 1 && kKPT <= 4, "D in {64, 128}");
+  static constexpr int kCH = D / 8;                  // 16-byte units of a row
+  static constexpr int kKPT = kBN * kCH / kThreads;  // keys staged per thread
+  static constexpr int kNKG = kBN / kKPT;            // key groups (threads per row part)
+  static_assert(kKPT >= 2 && kKPT <= 4, "D in {64, 128}");
 };
 
-// Physical position of key `key` (0..63) in row d of the transposed V tile.
+// LDS layouts (bank-conflict free for the MFMA operand reads with 32 or 64 banks, and for
+// the staging writes with 32 banks; modelled per access pattern before use).
+// K tile: row `key` of D elements, its 16-byte units XOR-swizzled by the key.
+template <int CH>
+__device__ __forceinline__ int k_unit(int key, int unit) {
+  return unit ^ ((key ^ (key >> 3)) & (CH - 1));
+}
+__device__ __forceinline__ int vt_swz(int d) { return (d ^ (d >> 3)) & 7; }
+
+// Column of key `key` (0..63) in row d of the transposed V tile. The 16-key chunk c0 is
+// stored as two 8-key units, unit 2 c0 + h holding keys {16c0 + 4h .. +3, 16c0 + 8 + 4h
+// .. +3} -- exactly the 8 k-values lane half h supplies to an MFMA operand -- so each
+// operand is one 16-byte read; units are XOR-swizzled by d.
 __device__ __forceinline__ int vt_col(int key, int d) {
-  return (((key >> 2) ^ ((d >> 1) & 15)) << 2) | (key & 3);
+  const int unit = ((key >> 4) << 1) | ((key >> 2) & 1);
+  const int within = (((key >> 3) & 1) << 2) | (key & 3);
+  return ((unit ^ vt_swz(d)) << 3) | within;
 }
 
 template <typename T, int D, int HG, int QB>
 __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const PrefillArgs a) {
   using Sh = PrefillShape<T, D>;
   using V8 = typename Mfma<T>::V8;
-  constexpr int CH = Sh::kCH, KPT = Sh::kKPT, KS = Sh::kKStride;
+  constexpr int CH = Sh::kCH, KPT = Sh::kKPT, NKG = Sh::kNKG;
   constexpr int BQ = 32 * QB;
   constexpr int DT = D / 32;  // 32-row output tiles
   constexpr int KC = D / 16;  // 16-wide MFMA k-chunks of the head dim
@@ -98,7 +110,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const Prefill
   // and P.V takes two MFMAs. fp16's 11 bits meet the tolerance with one.
   constexpr bool kSplitP = std::is_same_v<T, bf16>;
 
-  __shared__ __attribute__((aligned(16))) T k_lds[kBN * KS];
+  __shared__ __attribute__((aligned(16))) T k_lds[kBN * D];
   __shared__ __attribute__((aligned(16))) T vt_lds[D * kBN];
 
   const int tid = threadIdx.x;
@@ -147,12 +159,13 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const Prefill
   f32x16 oacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
-  float m_run = -1.0e30f;  // finite: 2^(m_run - score) underflows to exactly 0
+  float m_run = -1.0e30f;  // running max of scale*log2e*score; finite, so 2^(m_run - x) is 0
   float l_run = 0.f;       // this lane half's share of the softmax denominator
 
-  // Staging: thread tid copies row part p (8 elements) of keys 4 * kgrp .. + KPT - 1.
-  const int part = tid % CH;
-  const int kgrp = tid / CH;
+  // Staging: thread tid copies unit `part` (8 elements) of keys KPT * kgrp .. + KPT - 1,
+  // key groups fastest across lanes (so a transposed-V write spreads over the banks).
+  const int kgrp = tid % NKG;
+  const int part = tid / NKG;
   const int32_t* btrow = a.bt + static_cast<int64_t>(r) * a.bt_s;
   const T* kg = static_cast<const T*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh + part * 8;
   const T* vg = static_cast<const T*>(a.v) + static_cast<int64_t>(kvh) * a.k_sh + part * 8;
@@ -192,7 +205,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const Prefill
 #pragma unroll
     for (int u = 0; u < KPT; ++u) {
       const int key = kgrp * KPT + u;
-      store16(k_lds + key * KS + part * 8, kst[u]);
+      store16(k_lds + key * D + k_unit<CH>(key, part) * 8, kst[u]);
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -216,55 +229,74 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const Prefill
 
     if (n0 >= wave_key_end) continue;  // this wave's queries are all before the tile
 
-    // S^T = K . Q^T for the tile's two 32-key halves.
-    f32x16 sacc[2];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      sacc[sub] = f32x16{};
-      const T* kr = k_lds + (sub * 32 + col) * KS + 8 * half;
+    // S^T = K . Q^T for the tile's two 32-key halves: two independent MFMA chains.
+    f32x16 s0 = {}, s1 = {};
+    {
+      const T* kr0 = k_lds + col * D;
+      const T* kr1 = kr0 + 32 * D;
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        const V8 ka = *reinterpret_cast<const V8*>(kr + 16 * kc);
-        sacc[sub] = Mfma<T>::mma(ka, qreg[kc], sacc[sub]);
+        const int u0 = k_unit<CH>(col, 2 * kc + half), u1 = k_unit<CH>(col + 32, 2 * kc + half);
+        s0 = Mfma<T>::mma(*reinterpret_cast<const V8*>(kr0 + 8 * u0), qreg[kc], s0);
+        s1 = Mfma<T>::mma(*reinterpret_cast<const V8*>(kr1 + 8 * u1), qreg[kc], s1);
+      }
+    }
+    // Causal mask, only on a tile that crosses this wave's diagonal: item v of the lane
+    // holds key n0 + 8 (v / 4) + 4 half + v % 4 (+ 32 in s1).
+    if (n0 + kBN - 1 > wave_pos_min) {
+      const int lim = pos - n0 - 4 * half;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int kofs = 8 * (v >> 2) + (v & 3);
+        if (kofs > lim) s0[v] = -INFINITY;
+        if (kofs + 32 > lim) s1[v] = -INFINITY;
       }
     }
 
-    // Online softmax for this lane's query (base 2).
-    const bool need_mask = n0 + kBN - 1 > wave_pos_min;
-    float mx = -1.0e30f;
+    // Online softmax for this lane's query, in base 2 with the scale folded into one
+    // FMA: p = 2^(s * c - m), c = scale * log2(e) > 0, so max(s) * c = max(s * c).
+    float mx = fmaxf(s0[0], s1[0]);
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+    for (int v = 1; v < 16; ++v) mx = fmaxf(mx, fmaxf(s0[v], s1[v]));
+    mx = halves_max(mx);
+    const float m_new = fmaxf(m_run, mx * a.scale_log2);
+    if (__any(m_new > m_run)) {  // rescale only when some lane's maximum moved
+      const float alpha = fast_exp2(m_run - m_new);
+      l_run *= alpha;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        float s = sacc[sub][v] * a.scale_log2;
-        if (need_mask) {
-          const int key = n0 + sub * 32 + 8 * (v >> 2) + 4 * half + (v & 3);
-          if (key > pos) s = -INFINITY;
-        }
-        sacc[sub][v] = s;
-        mx = fmaxf(mx, s);
-      }
-    mx = fmaxf(mx, xor_lane<32>(mx));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
+      for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+      m_run = m_new;
+    }
+    const float neg_m = -m_run;
+    const float c = a.scale_log2;
     float psum = 0.f;
     V8 pk[4];
     V8 pk_lo[kSplitP ? 4 : 1];
+    typedef float F2 __attribute__((ext_vector_type(2)));
+    typedef T T2 __attribute__((ext_vector_type(2)));
+    typedef T T4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int c0 = 0; c0 < 4; ++c0) {
+      const f32x16& sv = (c0 < 2) ? s0 : s1;
+      T2 h[4], lo[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float p = fast_exp2(sacc[c0 >> 1][8 * (c0 & 1) + e] - m_new);
-        psum += p;
-        const T hi = static_cast<T>(p);
-        pk[c0][e] = hi;
-        if constexpr (kSplitP) pk_lo[c0][e] = static_cast<T>(p - static_cast<float>(hi));
+      for (int e2 = 0; e2 < 4; ++e2) {
+        const int v = 8 * (c0 & 1) + 2 * e2;
+        const F2 pf = {fast_exp2(fmaf(sv[v], c, neg_m)), fast_exp2(fmaf(sv[v + 1], c, neg_m))};
+        psum += pf[0] + pf[1];
+        h[e2] = __builtin_convertvector(pf, T2);
+        if constexpr (kSplitP) lo[e2] = __builtin_convertvector(pf - __builtin_convertvector(h[e2], F2), T2);
+      }
+      const T4 a01 = __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3);
+      const T4 a23 = __builtin_shufflevector(h[2], h[3], 0, 1, 2, 3);
+      pk[c0] = __builtin_shufflevector(a01, a23, 0, 1, 2, 3, 4, 5, 6, 7);
+      if constexpr (kSplitP) {
+        const T4 b01 = __builtin_shufflevector(lo[0], lo[1], 0, 1, 2, 3);
+        const T4 b23 = __builtin_shufflevector(lo[2], lo[3], 0, 1, 2, 3);
+        pk_lo[c0] = __builtin_shufflevector(b01, b23, 0, 1, 2, 3, 4, 5, 6, 7);
       }
     }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
+    l_run += psum;
 
     // O^T += V^T . P^T.
 #pragma unroll
@@ -273,17 +305,14 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const Prefill
       const T* vr = vt_lds + d * kBN;
 #pragma unroll
       for (int c0 = 0; c0 < 4; ++c0) {
-        typedef T T4 __attribute__((ext_vector_type(4)));
-        const T4 lo = *reinterpret_cast<const T4*>(vr + vt_col(16 * c0 + 4 * half, d));
-        const T4 hi = *reinterpret_cast<const T4*>(vr + vt_col(16 * c0 + 8 + 4 * half, d));
-        const V8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        const V8 va = *reinterpret_cast<const V8*>(vr + (((2 * c0 + half) ^ vt_swz(d)) << 3));
         oacc[dt] = Mfma<T>::mma(va, pk[c0], oacc[dt]);
         if constexpr (kSplitP) oacc[dt] = Mfma<T>::mma(va, pk_lo[c0], oacc[dt]);
       }
     }
   }
 
-  const float l_tot = l_run + xor_lane<32>(l_run);
+  const float l_tot = halves_sum(l_run);
   if (!q_ok) return;
   T* op = static_cast<T*>(a.out) + static_cast<int64_t>(q_start + qi) * a.o_st +
           static_cast<int64_t>(head) * a.o_sh;
