@@ -11,12 +11,14 @@ the entry points raise instead of computing anything on the CPU.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().with_name("libtinyserve_amd.so")
+# The in-tree build; TINYSERVE_AMD_LIB may name another build of the same sources.
+LIB_PATH = Path(os.environ.get("TINYSERVE_AMD_LIB") or Path(__file__).resolve().with_name("libtinyserve_amd.so"))
 
 _c_i32p = ctypes.POINTER(ctypes.c_int32)
 _c_i64p = ctypes.POINTER(ctypes.c_int64)

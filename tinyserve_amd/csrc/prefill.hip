@@ -5,23 +5,37 @@
 // last query position, online softmax, P rounded to the value dtype before P.V) and
 // src/tinyserve/attention.py:62-111 for the math it must equal.
 //
-// Work decomposition. A workgroup of 4 wave64s owns one kv head of one sequence and
-// 32 * QB consecutive queries of HG of the kv head's query heads (HG * QB = 4): wave w
-// takes query head hg = w % HG and the 32 queries of block qb = w / HG. All four
-// waves share each 64-key tile of K and V, which the workgroup gathers from the paged
-// cache (slot = table[pos / bs] * bs + pos % bs) into LDS once.
+// Work decomposition. A workgroup of 8 wave64s owns one kv head of one sequence and
+// 32 * QB consecutive queries of HG of that kv head's query heads (HG * QB = 8): wave w
+// takes query head hg = w % HG and the 32 queries of block qb = w / HG. All eight waves
+// share each 64-key tile of K and V.
+//
+// Memory pipeline. K/V tiles are gathered from the paged cache (slot = table[pos / bs]
+// * bs + pos % bs) straight into LDS with gfx950's direct-to-LDS loads
+// (global_load_lds_dwordx4: lane l's 16 bytes land at the instruction's LDS base +
+// 16 l), through a ring of three stages: while tile t is computed, tiles t + 1 and t + 2
+// are in flight. No registers stage the data and no LDS store instructions are issued.
+// Block-table entries are read with scalar loads, so the vector-memory counter covers
+// exactly the ring's loads and each stage is waited for with an exact vmcnt.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_{f16,bf16}). Scores are computed transposed,
-// S^T[key, query] = K . Q^T, with K as the A operand (from LDS, 16 contiguous bytes of a
-// key row per lane) and Q^T as the B operand (held in registers for the whole kernel).
-// In the 32x32 accumulator layout lane l holds column l % 32 -- one query -- and rows
-// (keys) 8j + 4(l / 32) + i at item 4j + i, so each lane owns 16 of its query's scores
-// per 32 keys: the softmax max/sum are in-lane plus one exchange between the lane halves.
-// The output is accumulated transposed too, O^T[d, query] += V^T . P^T: P^T is the B
-// operand straight from the score registers (lane half h supplies keys
-// {4h..4h+3, 8+4h..8+4h+3} of each 16-key chunk, an order the A operand repeats), and
-// V^T is the A operand, read from a transposed copy of the V tile in LDS (key-major per
-// d row, 4-key groups XOR-swizzled by d to spread the reads over the banks).
+// S^T[key, query] = K . Q^T, with K as the A operand (one 16-byte LDS read per lane) and
+// Q^T as the B operand (held in registers for the whole kernel). In the 32x32
+// accumulator layout lane l holds column l % 32 -- one query -- and rows (keys)
+// 8j + 4(l / 32) + i at item 4j + i, so each lane owns 16 of its query's scores per 32
+// keys: the softmax max/sum are in-lane plus one exchange between the lane halves. The
+// output is accumulated transposed too, O^T[d, query] += V^T . P^T: P^T is the B operand
+// straight from the score registers (lane half h supplies keys {4h..4h+3, 8+4h..8+4h+3}
+// of each 16-key chunk), and V^T is the A operand, read from the row-major V tile with
+// two ds_read_b64_tr_b16 per MFMA. That instruction works on groups of 16 lanes: lane j
+// of a group reads 4 consecutive 16-bit values ("row j") and lane i receives element
+// i % 4 of rows i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4. Pointing lane j at
+// V[key0 + j / 4][d0 + 4 (j % 4)] gives lane i the values V[key0 .. key0 + 3][d0 + i]:
+// four keys of one d, the transposed operand.
+//
+// LDS layout: K and V tiles are [64 keys][D], rows unpadded, their 16-byte units
+// XOR-swizzled per row (K by row & 15, V by a 4-row pattern), which keeps the K operand
+// reads and the transposing V reads free of bank conflicts.
 #include <type_traits>
 
 #include "common.h"
@@ -31,6 +45,11 @@ namespace ts {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+
+#define TS_LDS __attribute__((address_space(3)))
+#define TS_CONST __attribute__((address_space(4)))
 
 template <typename T>
 struct Mfma;
@@ -67,55 +86,98 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-constexpr int kBN = 64;        // keys per LDS tile
-constexpr int kThreads = 256;  // 4 waves
+constexpr int kBN = 64;     // keys per tile
+constexpr int kWaves = 8;   // waves per workgroup
+constexpr int kWin = 512;   // block ids held in LDS
 
-template <typename T, int D>
-struct PrefillShape {
-  static constexpr int kCH = D / 8;                  // 16-byte units of a row
-  static constexpr int kKPT = kBN * kCH / kThreads;  // keys staged per thread
-  static constexpr int kNKG = kBN / kKPT;            // key groups (threads per row part)
-  static_assert(kKPT >= 2 && kKPT <= 4, "D in {64, 128}");
+template <int D>
+struct TileShape {
+  static constexpr int kUPR = D / 8;                // 16-byte units per row
+  static constexpr int kRPI = kWave / kUPR;         // rows one direct-to-LDS instruction fills
+  static constexpr int kIPW = kBN / kRPI / kWaves;  // such instructions per wave per tensor
+  static_assert(kIPW >= 1 && kIPW * kRPI * kWaves == kBN, "D in {64, 128}");
 };
 
-// LDS layouts (bank-conflict free for the MFMA operand reads with 32 or 64 banks, and for
-// the staging writes with 32 banks; modelled per access pattern before use).
-// K tile: row `key` of D elements, its 16-byte units XOR-swizzled by the key.
-template <int CH>
-__device__ __forceinline__ int k_unit(int key, int unit) {
-  return unit ^ ((key ^ (key >> 3)) & (CH - 1));
+// Physical 16-byte unit of data unit u in row `row` of a tile is u ^ swz(row).
+template <int D>
+__device__ __forceinline__ int k_swz(int row) {
+  return row & (D / 8 - 1);
 }
-__device__ __forceinline__ int vt_swz(int d) { return (d ^ (d >> 3)) & 7; }
+template <int D>
+__device__ __forceinline__ int v_swz(int row) {
+  // 4-row patterns: {0, 6, 10, 12} for 16-unit rows, {0, 6, 4, 2} for 8-unit rows.
+  constexpr uint32_t kTab = D == 128 ? 0x0C0A0600u : 0x02040600u;
+  return (kTab >> ((row & 3) * 8)) & 0xFF;
+}
 
-// Column of key `key` (0..63) in row d of the transposed V tile. The 16-key chunk c0 is
-// stored as two 8-key units, unit 2 c0 + h holding keys {16c0 + 4h .. +3, 16c0 + 8 + 4h
-// .. +3} -- exactly the 8 k-values lane half h supplies to an MFMA operand -- so each
-// operand is one 16-byte read; units are XOR-swizzled by d.
-__device__ __forceinline__ int vt_col(int key, int d) {
-  const int unit = ((key >> 4) << 1) | ((key >> 2) & 1);
-  const int within = (((key >> 3) & 1) << 2) | (key & 3);
-  return ((unit ^ vt_swz(d)) << 3) | within;
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+
+// One direct-to-LDS load of 16 bytes per lane (global_load_lds_dwordx4; M0 holds the
+// LDS base). Issued as inline asm on purpose: the compiler's wait-count pass would
+// otherwise guard every later LDS read with a wait for all such loads in flight (it
+// cannot tell ring stages apart), draining the ring each step. The kernel orders these
+// loads itself with counted waits before every ring barrier; loads the compiler does not
+// count can only make its own waits stricter. Only the device pass sees the asm.
+__device__ __forceinline__ void lds_load16(const void* src, TS_LDS void* dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  // M0 is reserved to the compiler: the asm saves and restores it around the load.
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(src)
+      : "memory");
+#endif
+}
+
+// Wait until at most N of this wave's vector-memory operations are in flight and all its
+// LDS operations are done, then meet the other waves at s_barrier. __syncthreads() would
+// also fence workgroup memory, which waits for every load in flight (vmcnt(0)) and so
+// drains the ring; the tiles' visibility needs only each wave's own counted wait. The
+// signal fences (no instructions) keep the compiler from moving memory accesses across.
+template <int N>
+__device__ __forceinline__ void ring_barrier() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0070 | N);  // vmcnt N, expcnt 7 (no wait), lgkmcnt 0
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 template <typename T, int D, int HG, int QB>
-__global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const PrefillArgs a) {
-  using Sh = PrefillShape<T, D>;
+__global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+prefill_mfma_kernel(const PrefillArgs a) {
   using V8 = typename Mfma<T>::V8;
-  constexpr int CH = Sh::kCH, KPT = Sh::kKPT, NKG = Sh::kNKG;
+  using Sh = TileShape<D>;
+  constexpr int UPR = Sh::kUPR, RPI = Sh::kRPI, IPW = Sh::kIPW;
   constexpr int BQ = 32 * QB;
   constexpr int DT = D / 32;  // 32-row output tiles
   constexpr int KC = D / 16;  // 16-wide MFMA k-chunks of the head dim
+  constexpr int TILE = kBN * D;
+  constexpr int DMA_PER_TILE = 2 * IPW;  // direct-to-LDS instructions per wave per tile
+  constexpr float kRescale = 8.0f;
   // bf16 keeps 8 significant bits: P rounded once would move outputs by up to ~1e-2
   // against the fp32 reference, so P is carried as hi + lo bf16 parts (about 16 bits)
   // and P.V takes two MFMAs. fp16's 11 bits meet the tolerance with one.
   constexpr bool kSplitP = std::is_same_v<T, bf16>;
 
-  __shared__ __attribute__((aligned(16))) T k_lds[kBN * D];
-  __shared__ __attribute__((aligned(16))) T vt_lds[D * kBN];
+  __shared__ __attribute__((aligned(16))) T k_st0[TILE];
+  __shared__ __attribute__((aligned(16))) T k_st1[TILE];
+  __shared__ __attribute__((aligned(16))) T k_st2[TILE];
+  __shared__ __attribute__((aligned(16))) T v_st0[TILE];
+  __shared__ __attribute__((aligned(16))) T v_st1[TILE];
+  __shared__ __attribute__((aligned(16))) T v_st2[TILE];
+  __shared__ int32_t ids_lds[kWin];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31;  // this lane's query within the wave's 32
   const int half = lane >> 5;
 
@@ -139,6 +201,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const Prefill
   const bool q_ok = qi < q_len;
   const int pos = past + qi;
   const int key_end = past + min(q0 + BQ, q_len);  // keys the workgroup needs
+  const int key_last = key_end - 1;
   const int wave_key_end = wq0 < q_len ? past + min(wq0 + 32, q_len) : 0;
   const int wave_pos_min = past + wq0;
 
@@ -156,89 +219,93 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const Prefill
     }
   }
 
+  // Q is complete before the loop: without this wait the compiler re-checks the Q loads
+  // with a full vmcnt(0) at every step, which would also wait for the ring's loads.
+  __builtin_amdgcn_s_waitcnt(0x0070);
+
   f32x16 oacc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) oacc[dt] = f32x16{};
   float m_run = -1.0e30f;  // running max of scale*log2e*score; finite, so 2^(m_run - x) is 0
   float l_run = 0.f;       // this lane half's share of the softmax denominator
 
-  // Staging: thread tid copies unit `part` (8 elements) of keys KPT * kgrp .. + KPT - 1,
-  // key groups fastest across lanes (so a transposed-V write spreads over the banks).
-  const int kgrp = tid % NKG;
-  const int part = tid / NKG;
+  // ---- the gather: one tile of K and V into a ring stage --------------------------------
+  // Block ids of the keys [win_key0, win_key0 + kWin << lbs) sit in LDS, so a gather
+  // reads its ids with LDS loads and the vector-memory counter sees only the ring's
+  // loads. The window is refilled (with the ring drained) when a gather passes its end:
+  // every kWin blocks, i.e. never below 8192 keys for 16-slot blocks.
   const int32_t* btrow = a.bt + static_cast<int64_t>(r) * a.bt_s;
-  const T* kg = static_cast<const T*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh + part * 8;
-  const T* vg = static_cast<const T*>(a.v) + static_cast<int64_t>(kvh) * a.k_sh + part * 8;
-  const int bs_mask = (1 << a.lbs) - 1;
-
-  Pack16<T> kst[KPT], vst[KPT];
-  int btv[KPT];  // block-table entries of the tile after the one being loaded
-  auto fetch_bt = [&](int n0) {
-#pragma unroll
-    for (int u = 0; u < KPT; ++u) {
-      const int n = n0 + kgrp * KPT + u;
-      btv[u] = n < key_end ? btrow[n >> a.lbs] : 0;
+  const int lbs = a.lbs;
+  const int bs_mask = (1 << lbs) - 1;
+  const int nblk = (key_end + bs_mask) >> lbs;  // blocks holding keys 0 .. key_end - 1
+  int win_blk0 = 0;                              // first block id index in the window
+  auto fill_window = [&](int blk0) {
+    win_blk0 = blk0;
+    for (int i = tid; i < kWin; i += kWaves * kWave) {
+      const int j = min(blk0 + i, nblk - 1);
+      ids_lds[i] = btrow[j];
     }
   };
-  auto issue = [&](int n0) {
+  const T* kbase = static_cast<const T*>(a.k) + static_cast<int64_t>(kvh) * a.k_sh;
+  const T* vbase = static_cast<const T*>(a.v) + static_cast<int64_t>(kvh) * a.k_sh;
+  const int dma_row = lane / UPR;   // row within an instruction's RPI rows
+  const int dma_unit = lane % UPR;  // physical unit this lane fills
+
+  // Keys past key_end read key_last (finite, owned data): their scores are masked and
+  // their V rows meet P = 0.
+  auto gather = [&](T* k_lds, T* v_lds, int n0) {
 #pragma unroll
-    for (int u = 0; u < KPT; ++u) {
-      const int n = n0 + kgrp * KPT + u;
-      if (n < key_end) {
-        const int64_t off =
-            ((static_cast<int64_t>(btv[u]) << a.lbs) + (n & bs_mask)) * a.k_ss;
-        kst[u] = load16(kg + off);
-        vst[u] = load16(vg + off);
-      } else {
-        kst[u].raw = u32x4{0, 0, 0, 0};  // keys past the tile's need: zeros, never NaN
-        vst[u].raw = u32x4{0, 0, 0, 0};
-      }
+    for (int m = 0; m < IPW; ++m) {
+      const int row0 = (wave * IPW + m) * RPI;
+      const int row = row0 + dma_row;
+      const int key = min(n0 + row, key_last);
+      const int blk = ids_lds[(key >> lbs) - win_blk0];
+      const int64_t slot = (static_cast<int64_t>(blk) << lbs) + (key & bs_mask);
+      const int64_t off = slot * a.k_ss;
+      lds_load16(kbase + off + 8 * (dma_unit ^ k_swz<D>(row)), (TS_LDS void*)(k_lds + row0 * D));
+      lds_load16(vbase + off + 8 * (dma_unit ^ v_swz<D>(row)), (TS_LDS void*)(v_lds + row0 * D));
     }
   };
+  // Whether the ids of keys up to min(n0 + kBN, key_end) - 1 lie in the window.
+  auto in_window = [&](int n0) {
+    return ((min(n0 + kBN, key_end) - 1) >> lbs) < win_blk0 + kWin;
+  };
 
-  fetch_bt(0);
-  issue(0);
-  if (kBN < key_end) fetch_bt(kBN);
+  // ---- per-lane constants of the operand reads -------------------------------------------
+  const int kphys = k_swz<D>(col);  // K rows col and col + 32 swizzle alike
+  // V^T operand: lane j of its 16-lane group points at V[key0 + j / 4][d0 + 4 (j % 4)].
+  const int vj = lane & 15;
+  const int vdsub = (lane >> 4) & 1;
+  const int vkey_lane = 4 * half + (vj >> 2);     // + 16 c0 + 8 t
+  const int vd_lane = 16 * vdsub + 4 * (vj & 3);  // + 32 dt
+  const int vswz = v_swz<D>(vkey_lane);           // key & 3 = vj >> 2 for every read
 
-  for (int n0 = 0; n0 < key_end; n0 += kBN) {
-    __syncthreads();  // every wave is done reading the previous tile
-#pragma unroll
-    for (int u = 0; u < KPT; ++u) {
-      const int key = kgrp * KPT + u;
-      store16(k_lds + key * D + k_unit<CH>(key, part) * 8, kst[u]);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = part * 8 + e;
-      T* row = vt_lds + d * kBN;
-      if constexpr (KPT == 4) {
-        typedef T T4 __attribute__((ext_vector_type(4)));
-        T4 x = {vst[0].v[e], vst[1].v[e], vst[2].v[e], vst[3].v[e]};
-        *reinterpret_cast<T4*>(row + vt_col(kgrp * 4, d)) = x;
-      } else {
-        typedef T T2 __attribute__((ext_vector_type(2)));
-        T2 x = {vst[0].v[e], vst[1].v[e]};
-        *reinterpret_cast<T2*>(row + vt_col(kgrp * 2, d)) = x;
-      }
-    }
-    __syncthreads();
-    if (n0 + kBN < key_end) {
-      issue(n0 + kBN);
-      if (n0 + 2 * kBN < key_end) fetch_bt(n0 + 2 * kBN);
-    }
-
-    if (n0 >= wave_key_end) continue;  // this wave's queries are all before the tile
-
+  auto attend = [&](const T* k_lds, const T* v_lds, int n0) {
     // S^T = K . Q^T for the tile's two 32-key halves: two independent MFMA chains.
+    // The K operands of chunk kc + 1 are read while chunk kc multiplies.
     f32x16 s0 = {}, s1 = {};
     {
       const T* kr0 = k_lds + col * D;
       const T* kr1 = kr0 + 32 * D;
+      auto kread = [&](int kc, V8& x0, V8& x1) {
+        const int u = ((2 * kc + half) ^ kphys) * 8;
+        x0 = *reinterpret_cast<const V8*>(kr0 + u);
+        x1 = *reinterpret_cast<const V8*>(kr1 + u);
+      };
+      V8 ka[2][2];
+      kread(0, ka[0][0], ka[0][1]);
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        const int u0 = k_unit<CH>(col, 2 * kc + half), u1 = k_unit<CH>(col + 32, 2 * kc + half);
-        s0 = Mfma<T>::mma(*reinterpret_cast<const V8*>(kr0 + 8 * u0), qreg[kc], s0);
-        s1 = Mfma<T>::mma(*reinterpret_cast<const V8*>(kr1 + 8 * u1), qreg[kc], s1);
+        if (kc + 1 < KC) kread(kc + 1, ka[(kc + 1) & 1][0], ka[(kc + 1) & 1][1]);
+        s0 = Mfma<T>::mma(ka[kc & 1][0], qreg[kc], s0);
+        s1 = Mfma<T>::mma(ka[kc & 1][1], qreg[kc], s1);
+      }
+      // Keep that order through scheduling: reads of chunk kc + 1, then MFMAs of kc.
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        if (kc + 1 < KC) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
       }
     }
     // Causal mask, only on a tile that crosses this wave's diagonal: item v of the lane
@@ -259,8 +326,12 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const Prefill
 #pragma unroll
     for (int v = 1; v < 16; ++v) mx = fmaxf(mx, fmaxf(s0[v], s1[v]));
     mx = halves_max(mx);
-    const float m_new = fmaxf(m_run, mx * a.scale_log2);
-    if (__any(m_new > m_run)) {  // rescale only when some lane's maximum moved
+    mx *= a.scale_log2;
+    // Lazy rescaling: O and l are rescaled only when some lane's running maximum grows
+    // by more than kRescale (base 2); otherwise P = 2^(s c - m) uses the older, smaller
+    // m and stays below 2^kRescale, exact in fp32 and representable in fp16/bf16.
+    if (__any(mx > m_run + kRescale)) {
+      const float m_new = fmaxf(m_run, mx);
       const float alpha = fast_exp2(m_run - m_new);
       l_run *= alpha;
 #pragma unroll
@@ -285,7 +356,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const Prefill
         const F2 pf = {fast_exp2(fmaf(sv[v], c, neg_m)), fast_exp2(fmaf(sv[v + 1], c, neg_m))};
         psum += pf[0] + pf[1];
         h[e2] = __builtin_convertvector(pf, T2);
-        if constexpr (kSplitP) lo[e2] = __builtin_convertvector(pf - __builtin_convertvector(h[e2], F2), T2);
+        if constexpr (kSplitP)
+          lo[e2] = __builtin_convertvector(pf - __builtin_convertvector(h[e2], F2), T2);
       }
       const T4 a01 = __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3);
       const T4 a23 = __builtin_shufflevector(h[2], h[3], 0, 1, 2, 3);
@@ -298,19 +370,71 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const Prefill
     }
     l_run += psum;
 
-    // O^T += V^T . P^T.
+    // O^T += V^T . P^T, the V^T operand by two transposing reads per MFMA; the operand
+    // of step i + 1 is read while step i multiplies (step i = (dt, c0), c0 fastest).
+    auto vread = [&](int i) -> V8 {
+      const int dt = i >> 2, c0 = i & 3;
+      const int d = dt * 32 + vd_lane;
+      s16x4 part[2];
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const int d = dt * 32 + col;
-      const T* vr = vt_lds + d * kBN;
-#pragma unroll
-      for (int c0 = 0; c0 < 4; ++c0) {
-        const V8 va = *reinterpret_cast<const V8*>(vr + (((2 * c0 + half) ^ vt_swz(d)) << 3));
-        oacc[dt] = Mfma<T>::mma(va, pk[c0], oacc[dt]);
-        if constexpr (kSplitP) oacc[dt] = Mfma<T>::mma(va, pk_lo[c0], oacc[dt]);
+      for (int t = 0; t < 2; ++t) {
+        const int key = 16 * c0 + 8 * t + vkey_lane;
+        const T* p = v_lds + key * D + (((d >> 3) ^ vswz) << 3) + (d & 7);
+        part[t] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TS_LDS s16x4*)(p));
       }
+      return __builtin_bit_cast(V8, __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    V8 va[2];
+    va[0] = vread(0);
+#pragma unroll
+    for (int i = 0; i < 4 * DT; ++i) {
+      if (i + 1 < 4 * DT) va[(i + 1) & 1] = vread(i + 1);
+      const int dt = i >> 2, c0 = i & 3;
+      oacc[dt] = Mfma<T>::mma(va[i & 1], pk[c0], oacc[dt]);
+      if constexpr (kSplitP) oacc[dt] = Mfma<T>::mma(va[i & 1], pk_lo[c0], oacc[dt]);
     }
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+#pragma unroll
+    for (int i = 0; i < 4 * DT; ++i) {
+      if (i + 1 < 4 * DT) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, kSplitP ? 2 : 1, 1);
+    }
+  };
+
+  // ---- the ring: tile t lives in stage t % 3 -------------------------------------------------
+  // Before computing tile t a wave waits for its own loads of tile t (the loads of tile
+  // t + 1, if issued, may stay in flight), then the barrier makes every wave's loads of
+  // tile t visible and certifies that all waves finished tile t - 1, whose stage
+  // receives tile t + 2.
+  auto step = [&](const T* k_cur, const T* v_cur, T* k_next2, T* v_next2, int n0) {
+    if (n0 + kBN < key_end) ring_barrier<DMA_PER_TILE>();
+    else ring_barrier<0>();
+    const int n2 = n0 + 2 * kBN;
+    if (n2 < key_end) {
+      if (!in_window(n2)) {  // rare: drain, move the window to the gather's first block
+        __builtin_amdgcn_s_waitcnt(0x0070);
+        __syncthreads();
+        fill_window(n2 >> lbs);
+        __syncthreads();
+      }
+      gather(k_next2, v_next2, n2);
+    }
+    if (n0 < wave_key_end) attend(k_cur, v_cur, n0);
+  };
+
+  fill_window(0);
+  __syncthreads();
+  gather(k_st0, v_st0, 0);
+  if (kBN < key_end) gather(k_st1, v_st1, kBN);
+  for (int n0 = 0; n0 < key_end; n0 += 3 * kBN) {
+    step(k_st0, v_st0, k_st2, v_st2, n0);
+    if (n0 + kBN >= key_end) break;
+    step(k_st1, v_st1, k_st0, v_st0, n0 + kBN);
+    if (n0 + 2 * kBN >= key_end) break;
+    step(k_st2, v_st2, k_st1, v_st1, n0 + 2 * kBN);
   }
+  // No load may still be writing this workgroup's LDS when its waves end.
+  __builtin_amdgcn_s_waitcnt(0x0070);
 
   const float l_tot = halves_sum(l_run);
   if (!q_ok) return;
@@ -331,22 +455,23 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_mfma_kernel(const Prefill
 
 template <typename T, int D, int HG>
 static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream) {
-  constexpr int QB = 4 / HG;
+  constexpr int QB = kWaves / HG;
   dim3 grid(static_cast<unsigned>(a.n_qtiles) * a.R, Hkv * a.hchunks);
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB>), grid, dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB>), grid, dim3(kWaves * kWave), 0, stream, a);
   return launch_status();
 }
 
 template <typename T, int D>
 static int dispatch_hg(PrefillArgs& a, int Hkv, int max_q_len, hipStream_t stream) {
-  const int hg = a.group < 4 ? a.group : 4;
+  const int hg = a.group < kWaves ? a.group : kWaves;
   a.hchunks = a.group / hg;
-  const int bq = 32 * (4 / hg);
+  const int bq = 32 * (kWaves / hg);
   a.n_qtiles = (max_q_len + bq - 1) / bq;
   switch (hg) {
     case 1: return launch_prefill_mfma<T, D, 1>(a, Hkv, stream);
     case 2: return launch_prefill_mfma<T, D, 2>(a, Hkv, stream);
     case 4: return launch_prefill_mfma<T, D, 4>(a, Hkv, stream);
+    case 8: return launch_prefill_mfma<T, D, 8>(a, Hkv, stream);
     default: return TS_EUNSUPPORTED;
   }
 }
@@ -376,7 +501,11 @@ extern "C" int ts_prefill_varlen(const void* q, const void* k_cache, const void*
   if (R == 0 || max_q_len == 0) return 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int lbs = ilog2(block_size);
-  if ((dtype == TS_F16 || dtype == TS_BF16) && (D == 64 || D == 128)) {
+  // The direct-to-LDS gather moves 16-byte units: rows must start 16-byte aligned.
+  const bool aligned = (k_stride_slot % 8 == 0) && (k_stride_head % 8 == 0) &&
+                       (reinterpret_cast<uintptr_t>(k_cache) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(v_cache) % 16 == 0);
+  if ((dtype == TS_F16 || dtype == TS_BF16) && (D == 64 || D == 128) && aligned) {
     PrefillArgs a{q, k_cache, v_cache, out, block_tables, q_starts, q_lens, context_lens,
                   R, Hq / Hkv, 1, lbs, 1, q_stride_t, q_stride_h, o_stride_t, o_stride_h,
                   k_stride_slot, k_stride_head, bt_stride, scale * kLog2e};
