@@ -3,11 +3,12 @@
 The headline ``value`` is the metric's workload: one layer's paged decode attention at
 B=64 sequences x 4096 tokens, fp16, Qwen3-0.6B shapes (16 query / 8 kv heads, head_dim
 128, 16-token blocks scattered over the pool), split-K + combine. One step = one call
-of the split kernel and the combine kernel on inputs already resident in HBM. ``value``
+of the attention kernel (plus the combine kernel when the launch policy splits into HBM
+partials; at this batch it does not) on inputs already resident in HBM. ``value``
 is the step's algorithmic bytes (K and V read once, q read, out written, block tables
 and lengths read: 1,074,332,160 B) divided by the measured time per step, in GB/s.
 
-``roofline`` covers the dominant kernel (the split kernel): algorithmic bytes per launch
+``roofline`` covers the dominant kernel (the attention kernel): algorithmic bytes per launch
 / its average duration measured with HIP events on the launch stream, against the
 8 TB/s HBM peak. ``cpu_baseline`` times the CPU oracle (the PyTorch reference path,
 restated) on the same workload on this host's cores. ``extra`` adds the prefill
@@ -44,12 +45,15 @@ METRIC = "decode-attn HBM GB/s (% of peak) at B=64,ctx=4096; prefill-attn MFMA u
 HQ, HKV, D, BS = 16, 8, 128, 16
 
 
-def decode_bytes(b: int, ctx: int, esize: int = 2) -> dict[str, int]:
+def decode_bytes(b: int, ctx: int, splits: int = 1, esize: int = 2) -> dict[str, int]:
+    """Algorithmic bytes of one step, and of its attention kernel alone (which writes the
+    output itself with one split, fp32 partials for the combine otherwise)."""
     kv = b * ctx * HKV * D * 2 * esize
     q_io = 2 * b * HQ * D * esize
     tables = b * math.ceil(ctx / BS) * 4
     lens = b * 4
-    return {"step": kv + q_io + tables + lens, "split_kernel": kv + q_io // 2 + tables + lens}
+    step = kv + q_io + tables + lens
+    return {"step": step, "split_kernel": step if splits == 1 else step - q_io // 2}
 
 
 def split_kernel_launch(c, splits: int, m, l, acc, out, stream: int) -> None:
@@ -85,28 +89,33 @@ def time_decode(batch: int, ctx: int, splits: int, steps: int, warmup: int) -> d
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    # Timed region: exactly `steps` steps, with events around every split launch.
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]  # fmt: skip
+    # Timed region: exactly `steps` steps, one event pair around all of them (an event
+    # per launch would add a gap between launches).
     t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     t_start.record(stream)
-    for a, b in ev:
-        a.record(stream)
-        split_kernel_launch(c, splits, m, l, acc, out, s)
-        b.record(stream)
-        if splits > 1:
-            combine_launch(splits, m, l, acc, out, s)
+    for _ in range(steps):
+        step()
     t_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_start.elapsed_time(t_end)
-    split_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+    if splits == 1:
+        split_ms = total_ms / steps  # the step is the attention kernel alone
+    else:
+        # The attention kernel alone, `steps` back-to-back launches on the same stream.
+        t_start.record(stream)
+        for _ in range(steps):
+            split_kernel_launch(c, splits, m, l, acc, out, s)
+        t_end.record(stream)
+        torch.cuda.synchronize()
+        split_ms = t_start.elapsed_time(t_end) / steps
+        combine_launch(splits, m, l, acc, out, s)
     # The public entry point gives the same result (a check, outside the timed region).
     ref_out = launch_paged_decode_split(*c.args(), c.scale, BS, num_splits=splits)
     assert torch.equal(ref_out, out), "bench launch differs from the entry point"
-    nbytes = decode_bytes(batch, ctx)
+    nbytes = decode_bytes(batch, ctx, splits)
     return {"ms_per_step": total_ms / steps, "wall_ms_per_step": wall * 1e3 / steps,
             "split_ms": split_ms, "bytes": nbytes, "case": c}  # fmt: skip
 
@@ -124,7 +133,7 @@ def loop_ms(fn, iters: int = 20, warmup: int = 3) -> float:
     return a.elapsed_time(b) / iters
 
 
-def cpu_baseline(case, splits: int, budget_s: float = 12.0) -> dict:
+def cpu_baseline(case, splits: int, budget_s: float = 15.0) -> dict:
     """The oracle (PyTorch reference path restated) on this host, over the same 64 x 4096
     workload, repeated until ``budget_s`` of work (at least once)."""
     from oracle import ref
@@ -137,7 +146,7 @@ def cpu_baseline(case, splits: int, budget_s: float = 12.0) -> dict:
     while True:
         ref.decode_ref(q, kc, vc, bt, lens, case.scale, BS)
         reps += 1
-        if time.perf_counter() - t0 >= budget_s or reps >= 5:
+        if time.perf_counter() - t0 >= budget_s or reps >= 100:
             break
     dt = (time.perf_counter() - t0) / reps
     nbytes = decode_bytes(q.shape[0], int(lens[0]))["step"]
@@ -197,6 +206,9 @@ def main() -> None:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="also run 3 plain device copies of this many MiB (a known-size kernel "
+                         "that calibrates the HBM byte counters of a profiler)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -213,8 +225,8 @@ def main() -> None:
     value = step_bytes / r["ms_per_step"] / 1e6  # GB/s
     achieved = split_bytes / r["split_ms"] / 1e6
     traffic = None
-    tf = ROOT / "profiles" / "decode_split_b64_ctx4096_traffic.json"
-    if tf.exists():
+    tf = ROOT / "profiles" / "paged_attend_decode_b64_ctx4096_traffic.json"
+    if tf.exists() and (args.batch, args.ctx, splits) == (64, 4096, 1):
         traffic = json.loads(tf.read_text()).get("bytes_per_launch")
     line = {
         "metric": METRIC,
@@ -227,13 +239,15 @@ def main() -> None:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16 (fp32 accumulate)",
+        "dtype": "f16",
         "data": "synthetic: K/V/q ~ N(0,1), block tables a random permutation of the pool",
         "config": {"workload": f"paged decode attention, one layer, B={args.batch} x ctx={args.ctx}, "
-                               f"16 q / 8 kv heads, head_dim 128, block 16, split-K {splits} + combine",
+                               f"16 q / 8 kv heads, head_dim 128, block 16, "
+                               + ("one launch (in-workgroup split-K)" if splits == 1
+                                  else f"split-K {splits} + combine"),
                    "batch": args.batch, "ctx": args.ctx, "splits": splits,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "paged_attend_kernel (split)",
+        "roofline": {"bound": "hbm", "kernel": "paged_attend_kernel<f16,128,2,false>",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "avg_launch_us": round(r["split_ms"] * 1e3, 2),
@@ -244,6 +258,13 @@ def main() -> None:
         line["cpu_baseline"] = cpu_baseline(r["case"], splits)
     if not args.no_extra:
         line["extra"] = extra_measurements()
+    if args.copy_mb:
+        src = torch.ones(args.copy_mb << 18, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["copy_calibration_bytes"] = {"read": src.numel() * 4, "write": dst.numel() * 4}
     print(json.dumps(line), flush=True)
 
 

@@ -218,3 +218,18 @@ def test_metric_size_batch(dtype: torch.dtype) -> None:
         sub = DecodeCase(c.q[b : b + 1].cpu(), kc, vc, c.block_tables[b : b + 1].cpu(),
                          c.context_lens[b : b + 1].cpu(), c.scale, c.block_size)  # fmt: skip
         assert_matches(outs[8][b : b + 1], oracle32(sub), dtype, f"seq {b}")
+
+
+@pytest.mark.parametrize("batch", [20, 40, 80])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_every_workgroup_width_gives_the_reference(batch: int, splits: int) -> None:
+    # The library runs each (sequence, head tile, split) on a workgroup of 1, 2 or 4 waves
+    # that merge in LDS, chosen from the grid size (about 1024 waves in all on 256 CUs):
+    # at Qwen3 shapes (8 head tiles) 80 sequences take 1 wave each, 40 take 2, 20 take 4.
+    lens = [1 + (37 * i) % 300 for i in range(batch)]
+    c = decode_case(lens, dtype=torch.float16, seed=batch + splits)
+    want = oracle32(c)
+    g = on_gpu(c)
+    out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, num_splits=splits)
+    assert torch.isfinite(out).all()
+    assert_matches(out, want, torch.float16, f"B={batch} splits={splits}")

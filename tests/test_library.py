@@ -141,10 +141,10 @@ def test_split_policy_tables() -> None:
     assert hip_attention.num_splits_for(1, 8, 4, **t4) == 4
     assert hip_attention.num_splits_for(1, 1, 64, **t4) == hip_attention.MAX_SPLITS
     assert hip_attention.num_splits_for(256, 1, 64, **t4) == 1
-    # ... and the MI355X default: about 4096 waves, never more than the table width.
-    assert [hip_attention.num_splits_for(b, 8, 256) for b in (1, 8, 32, 64, 128, 512)] == [
-        16, 16, 16, 8, 4, 1]  # fmt: skip
-    assert hip_attention.num_splits_for(64, 8, 4) == 4
+    # ... and the MI355X default: about 256 workgroups, never more than the table width.
+    assert [hip_attention.num_splits_for(b, 8, 256) for b in (1, 8, 16, 32, 64, 512)] == [
+        16, 4, 2, 1, 1, 1]  # fmt: skip
+    assert hip_attention.num_splits_for(1, 8, 4) == 4
 
 
 # --- prefill and fused argument errors (test_triton_prefill.py:173-185,

@@ -3,6 +3,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 #include <stdint.h>
 
 #include "../../include/tinyserve_amd.h"
@@ -99,6 +101,22 @@ inline int ilog2(int x) {
 inline bool is_pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
 inline int elem_size(int dtype) { return dtype == TS_F32 ? 4 : 2; }
+
+// Compute units of the current device (cached per device; 256 on MI355X).
+inline int compute_units() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64) {
+    const int hit = cache[dev].load(std::memory_order_relaxed);
+    if (hit > 0) return hit;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
 
 inline int launch_status() {
   hipError_t e = hipGetLastError();

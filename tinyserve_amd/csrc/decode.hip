@@ -13,6 +13,13 @@
 // 4 KB of K and 4 KB of V per wave per iteration, both issued before the previous
 // iteration's math so that two iterations are always in flight).
 //
+// Waves per workgroup. A decode launch gives each (sequence, head tile, split) a
+// workgroup of W = 1, 2 or 4 waves; wave w takes the w-th of W contiguous block ranges of
+// the split's range, and the W partial states are merged through LDS before anything is
+// written. This is split-K without HBM partials or a second launch: the library picks W
+// so that the grid holds about four waves per CU (the kernel needs more than 256 VGPRs,
+// so a SIMD runs one wave of it, and a CU wants four in flight to cover HBM latency).
+//
 // Softmax. Every token lane keeps its own running (max, sum, acc) per query head (the
 // online softmax of triton_attention.py:14-22, in base 2), so the loop has no
 // cross-lane work except the LPT-lane dot-product reduction. The token lanes are
@@ -20,12 +27,26 @@
 // l = 2^(m1-m) l1 + 2^(m2-m) l2 (same for acc), the rule the combine pass uses too.
 #include "common.h"
 
+// Bytes of a head row each lane streams per token, and the occupancy the register
+// budget is sized for (waves per SIMD).
+#ifndef TS_DECODE_LANE_BYTES
+#define TS_DECODE_LANE_BYTES 64
+#endif
+#ifndef TS_DECODE_NBUF
+#define TS_DECODE_NBUF 2
+#endif
+#ifndef TS_DECODE_WAVES_PER_EU
+#define TS_DECODE_WAVES_PER_EU 1
+#endif
+
 namespace ts {
 
 template <typename T, int D>
 struct RowShape {
   static constexpr int kRowBytes = D * static_cast<int>(sizeof(T));
-  static constexpr int kLPT = kRowBytes <= 64 ? 1 : (kRowBytes / 64 > 64 ? 64 : kRowBytes / 64);
+  static constexpr int kLaneBytes = TS_DECODE_LANE_BYTES;  // bytes of a row per lane
+  static constexpr int kLPT =
+      kRowBytes <= kLaneBytes ? 1 : (kRowBytes / kLaneBytes > 64 ? 64 : kRowBytes / kLaneBytes);
   static constexpr int kE = D / kLPT;
   static constexpr int kVec = 16 / static_cast<int>(sizeof(T));
   static constexpr int kNV = kE / kVec;
@@ -49,6 +70,7 @@ struct AttendArgs {
   int group;  // query heads per kv head
   int lbs;    // log2(block_size)
   int splits;
+  int wpg;        // waves per workgroup (decode), 1 for prefill
   int max_q_len;  // prefill only
   int64_t q_sb, q_sh, o_sb, o_sh, k_ss, k_sh, bt_s;
   float scale_log2;  // softmax scale * log2(e)
@@ -119,15 +141,72 @@ __device__ __forceinline__ void merge_token_lanes(TokenState<T, D, HT>& st) {
   if constexpr (L <= 32) merge_lanes<32>(st);
 }
 
+constexpr int kMaxWavesPerGroup = 4;
+
+// The W waves of a decode workgroup each hold a merged state (in their first LPT lanes,
+// lane c holding elements (i * LPT + c) * VEC + j). They park it in LDS, then thread t
+// of the group produces output element t (of HT * D) by the two-partial rule over the W
+// states, and writes it either as the final output (one split) or as the split's fp32
+// partial for the combine pass.
+template <typename T, int D, int HT, typename State, typename Args>
+__device__ __forceinline__ void merge_group_waves(const Args& a, const State& st, int wave,
+                                                  int c, int seq, int h0, int split,
+                                                  int64_t orow) {
+  using S = RowShape<T, D>;
+  constexpr int NV = S::kNV, VEC = S::kVec, LPT = S::kLPT;
+  __shared__ float sm[kMaxWavesPerGroup][HT], sl[kMaxWavesPerGroup][HT];
+  __shared__ float sacc[kMaxWavesPerGroup][HT][D];
+  if (c >= 0) {
+#pragma unroll
+    for (int g = 0; g < HT; ++g) {
+      if (c == 0) {
+        sm[wave][g] = st.m[g];
+        sl[wave][g] = st.l[g];
+      }
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) sacc[wave][g][(i * LPT + c) * VEC + j] = st.acc[g][i * VEC + j];
+    }
+  }
+  __syncthreads();
+  const int W = a.wpg;
+  for (int t = threadIdx.x; t < HT * D; t += W * kWave) {
+    const int g = t / D, d = t % D;
+    float mm = sm[0][g];
+    for (int w = 1; w < W; ++w) mm = fmaxf(mm, sm[w][g]);
+    float den = 0.f, num = 0.f;
+    for (int w = 0; w < W; ++w) {
+      const float f = fast_exp2(sm[w][g] - mm);
+      den = fmaf(f, sl[w][g], den);
+      num = fmaf(f, sacc[w][g][d], num);
+    }
+    if (a.splits == 1) {
+      static_cast<T*>(a.out)[orow + (h0 + g) * a.o_sh + d] = from_f32<T>(num / den);
+    } else {
+      const int64_t part = (static_cast<int64_t>(seq) * a.Hq + h0 + g) * a.splits + split;
+      if (d == 0) {
+        a.m[part] = den > 0.f ? mm : -INFINITY;
+        a.l[part] = den;
+      }
+      a.acc[part * D + d] = num;
+    }
+  }
+}
+
 // A finite "no score yet" maximum: 2^(kNoMax - real score) is exactly 0, and two empty
 // states merge to an empty state without inf - inf.
 constexpr float kNoMax = -1.0e30f;
 
 template <typename T, int D, int HT, bool PREFILL>
-__global__ __launch_bounds__(64) void paged_attend_kernel(const AttendArgs a) {
+__global__ __launch_bounds__(PREFILL ? kWave : kWave * kMaxWavesPerGroup)
+__attribute__((amdgpu_waves_per_eu(TS_DECODE_WAVES_PER_EU)))
+void paged_attend_kernel(const AttendArgs a) {
   using S = RowShape<T, D>;
   constexpr int LPT = S::kLPT, NV = S::kNV, VEC = S::kVec, TPW = S::kTPW, E = S::kE;
-  const int lane = threadIdx.x;
+  constexpr int NBUF = TS_DECODE_NBUF;
+  const int lane = threadIdx.x % kWave;
+  const int wave = PREFILL ? 0 : threadIdx.x / kWave;
   const int c = lane % LPT;
   const int tl = lane / LPT;
   const int h0 = blockIdx.y * HT;
@@ -154,8 +233,9 @@ __global__ __launch_bounds__(64) void paged_attend_kernel(const AttendArgs a) {
   const int lbs = a.lbs;
   const int bs_mask = (1 << lbs) - 1;
   const int nblocks = (ctx + bs_mask) >> lbs;
-  const int per = (nblocks + a.splits - 1) / a.splits;
-  const int first = split * per;
+  const int ranges = a.splits * a.wpg;
+  const int per = (nblocks + ranges - 1) / ranges;
+  const int first = (split * a.wpg + wave) * per;
   const int last = min(first + per, nblocks);
 
   const T* qp = static_cast<const T*>(a.q) + qrow;
@@ -186,7 +266,9 @@ __global__ __launch_bounds__(64) void paged_attend_kernel(const AttendArgs a) {
     int chunk = first;
     int win = (chunk + lane < last) ? btrow[chunk + lane] : 0;
 
-    Pack16<T> kc[NV], vc[NV], kn[NV], vn[NV];
+    // NBUF iterations in flight: the loads of iteration i + NBUF - 1 are issued before
+    // iteration i's math (ring of NBUF register buffers, indices fixed by unrolling).
+    Pack16<T> kb[NBUF][NV], vb[NBUF][NV];
     auto issue = [&](Pack16<T>(&kf)[NV], Pack16<T>(&vf)[NV], int p0) {
       if (((p0 >> lbs) - chunk) >= 64) {
         chunk += 64;
@@ -204,7 +286,6 @@ __global__ __launch_bounds__(64) void paged_attend_kernel(const AttendArgs a) {
         vf[i] = load16(vbase + off + i * LPT * VEC);
       }
     };
-
     auto attend = [&](const Pack16<T>(&kf)[NV], const Pack16<T>(&vf)[NV], int p0) {
       const bool valid = p0 + tl < t1;
       float s[HT];
@@ -245,23 +326,28 @@ __global__ __launch_bounds__(64) void paged_attend_kernel(const AttendArgs a) {
       }
     };
 
-    // Two iterations in flight: the next one's loads are issued before this one's math.
-    int p0 = t0;
-    issue(kc, vc, p0);
-    while (true) {
-      const int p1 = p0 + TPW;
-      if (p1 < t1) issue(kn, vn, p1);
-      attend(kc, vc, p0);
-      if (p1 >= t1) break;
-      const int p2 = p1 + TPW;
-      if (p2 < t1) issue(kc, vc, p2);
-      attend(kn, vn, p1);
-      if (p2 >= t1) break;
-      p0 = p2;
+#pragma unroll
+    for (int j = 0; j + 1 < NBUF; ++j)
+      if (t0 + j * TPW < t1) issue(kb[j], vb[j], t0 + j * TPW);
+    for (int base = t0; base < t1; base += NBUF * TPW) {
+#pragma unroll
+      for (int j = 0; j < NBUF; ++j) {
+        const int p0 = base + j * TPW;
+        if (p0 >= t1) break;
+        const int pn = p0 + (NBUF - 1) * TPW;
+        if (pn < t1) issue(kb[(j + NBUF - 1) % NBUF], vb[(j + NBUF - 1) % NBUF], pn);
+        attend(kb[j], vb[j], p0);
+      }
     }
   }
 
   merge_token_lanes(st);
+  if constexpr (!PREFILL) {
+    if (a.wpg > 1) {
+      merge_group_waves<T, D, HT>(a, st, wave, tl == 0 ? c : -1, seq, h0, split, orow);
+      return;
+    }
+  }
   if (tl != 0) return;
 
   if (PREFILL || a.splits == 1) {
@@ -319,7 +405,8 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ m
 
 template <typename T, int D, int HT, bool PREFILL>
 static int launch_attend(const AttendArgs& a, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, PREFILL>), grid, dim3(kWave), 0, stream, a);
+  hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, PREFILL>), grid, dim3(kWave * a.wpg), 0,
+                     stream, a);
   return launch_status();
 }
 
@@ -376,7 +463,7 @@ int prefill_rows_generic(const void* q, const void* k, const void* v, void* out,
   const int ht = head_tile_for(group, 0);
   if (ht < 0) return TS_EINVAL;
   AttendArgs a{q, k, v, bt, ctx_lens, out, nullptr, nullptr, nullptr, q_starts, q_lens,
-               Hq, group, lbs, 1, max_q_len, q_st, q_sh, o_st, o_sh, k_ss, k_sh, bt_s,
+               Hq, group, lbs, 1, 1, max_q_len, q_st, q_sh, o_st, o_sh, k_ss, k_sh, bt_s,
                scale * kLog2e};
   dim3 grid(static_cast<unsigned>(R) * max_q_len, Hq / ht, 1);
   return dispatch_attend<true>(a, dtype, D, ht, grid, stream);
@@ -402,8 +489,12 @@ extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v
   const int group = Hq / Hkv;
   const int ht = head_tile_for(group, head_tile);
   if (ht < 0) return TS_EINVAL;
+  const int64_t waves = static_cast<int64_t>(B) * (Hq / ht) * splits;
+  const int64_t want = 4 * static_cast<int64_t>(compute_units());
+  int wpg = 1;
+  while (wpg < kMaxWavesPerGroup && waves * wpg * 2 <= want) wpg *= 2;
   AttendArgs a{q, k_cache, v_cache, block_tables, context_lens, out, m, l, acc, nullptr,
-               nullptr, Hq, group, ilog2(block_size), splits, 0, q_stride_b, q_stride_h,
+               nullptr, Hq, group, ilog2(block_size), splits, wpg, 0, q_stride_b, q_stride_h,
                o_stride_b, o_stride_h, k_stride_slot, k_stride_head, bt_stride,
                scale * kLog2e};
   dim3 grid(B, Hq / ht, splits);

@@ -30,12 +30,16 @@ from tinyserve_amd import _lib
 NO_SPECIALIZE = ["stride_bt", "num_splits"]
 DECODE_TILE = (1, 1)
 
-# Split-K policy (the reference's :488-510, retuned for 256 CUs). A wave needs several
-# hundred KB of K/V in flight per CU to approach the HBM roofline, so the launch aims at
-# TARGET_PROGRAMS waves and stops splitting once the batch alone gives
-# NO_SPLIT_PROGRAMS. The reference's T4 values were 1024 and 256.
-TARGET_PROGRAMS = 4096
-NO_SPLIT_PROGRAMS = 4096
+# Split-K policy (the reference's :488-510, retuned for MI355X). The kernel runs one wave
+# per SIMD (it needs more than 256 VGPRs), and HBM wants about four waves per CU in
+# flight. The library already splits each (sequence, head tile, split) over a workgroup
+# of up to 4 waves that merge in LDS (no HBM partials, no second launch), so a launch of
+# 256 workgroups (one per CU) fills the chip. Splits that write HBM partials are only
+# added below that: the launch aims at TARGET_PROGRAMS workgroups and stops splitting
+# once the batch alone gives NO_SPLIT_PROGRAMS. The reference's T4 values were 1024 and
+# 256 (T4_* below).
+TARGET_PROGRAMS = 256
+NO_SPLIT_PROGRAMS = 256
 MAX_SPLITS = 16
 
 # Reference constants, kept for ``num_splits_for(..., target=..., no_split=...)`` callers
