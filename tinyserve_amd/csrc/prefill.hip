@@ -15,8 +15,15 @@
 // (global_load_lds_dwordx4: lane l's 16 bytes land at the instruction's LDS base +
 // 16 l), through a ring of three stages: while tile t is computed, tiles t + 1 and t + 2
 // are in flight. No registers stage the data and no LDS store instructions are issued.
-// Block-table entries are read with scalar loads, so the vector-memory counter covers
-// exactly the ring's loads and each stage is waited for with an exact vmcnt.
+// Block ids are staged in LDS (a window of 512 table entries, refilled when a gather
+// passes its end), so the vector-memory counter covers exactly the ring's loads and each
+// stage is waited for with an exact vmcnt.
+//
+// Dispatch order. Workgroup b = (tile_rev * R + r) * heads + head: every sequence's last
+// query tile (the one with the most keys) is dispatched, for all kv heads, before any
+// earlier tile, so the long-running workgroups start first; and since the hardware
+// deals workgroups to the 8 XCDs round-robin, with 8 kv heads each head's workgroups
+// share one XCD's L2, where its K/V blocks are re-read by every query tile.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_{f16,bf16}). Scores are computed transposed,
 // S^T[key, query] = K . Q^T, with K as the A operand (one 16-byte LDS read per lane) and
@@ -82,6 +89,7 @@ struct PrefillArgs {
   int hchunks;  // group / HG
   int lbs;
   int n_qtiles;
+  int n_kvh;
   int64_t q_st, q_sh, o_st, o_sh, k_ss, k_sh, bt_s;
   float scale_log2;
 };
@@ -181,16 +189,20 @@ prefill_mfma_kernel(const PrefillArgs a) {
   const int col = lane & 31;  // this lane's query within the wave's 32
   const int half = lane >> 5;
 
-  const int tile_rev = blockIdx.x / a.R;
-  const int r = blockIdx.x - tile_rev * a.R;
-  const int tile = a.n_qtiles - 1 - tile_rev;  // the longest-running tiles launch first
+  const int n_hc = a.n_kvh * a.hchunks;
+  const int bid = blockIdx.x;
+  const int rest = bid / n_hc;
+  const int hcx = bid - rest * n_hc;
+  const int tile_rev = rest / a.R;
+  const int r = rest - tile_rev * a.R;
   const int q_len = a.q_lens[r];
+  const int tile = (q_len + BQ - 1) / BQ - 1 - tile_rev;
+  if (tile < 0) return;
   const int q0 = tile * BQ;
-  if (q0 >= q_len) return;
   const int ctx = a.ctx_lens[r];
   const int q_start = a.q_starts[r];
-  const int kvh = blockIdx.y / a.hchunks;
-  const int hc = blockIdx.y - kvh * a.hchunks;
+  const int kvh = hcx / a.hchunks;
+  const int hc = hcx - kvh * a.hchunks;
   const int hg = wave % HG;
   const int qb = wave / HG;
   const int head = kvh * a.group + hc * HG + hg;
@@ -321,52 +333,64 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
 
     // Online softmax for this lane's query, in base 2 with the scale folded into one
-    // FMA: p = 2^(s * c - m), c = scale * log2(e) > 0, so max(s) * c = max(s * c).
-    float mx = fmaxf(s0[0], s1[0]);
+    // FMA: p = 2^(s * c - m), c = scale * log2(e) > 0.
+    const float c = a.scale_log2;
+    V8 pk[4];
+    V8 pk_lo[kSplitP ? 4 : 1];
+    typedef float F2 __attribute__((ext_vector_type(2)));
+    typedef T T2 __attribute__((ext_vector_type(2)));
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    // P^T of the tile against the running maximum m_run; returns this lane's sum of P.
+    auto make_p = [&]() -> float {
+      const float neg_m = -m_run;
+      float psum = 0.f;
 #pragma unroll
-    for (int v = 1; v < 16; ++v) mx = fmaxf(mx, fmaxf(s0[v], s1[v]));
-    mx = halves_max(mx);
-    mx *= a.scale_log2;
-    // Lazy rescaling: O and l are rescaled only when some lane's running maximum grows
-    // by more than kRescale (base 2); otherwise P = 2^(s c - m) uses the older, smaller
-    // m and stays below 2^kRescale, exact in fp32 and representable in fp16/bf16.
-    if (__any(mx > m_run + kRescale)) {
+      for (int c0 = 0; c0 < 4; ++c0) {
+        const f32x16& sv = (c0 < 2) ? s0 : s1;
+        T2 h[4], lo[4];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const int v = 8 * (c0 & 1) + 2 * e2;
+          const F2 pf = {fast_exp2(fmaf(sv[v], c, neg_m)), fast_exp2(fmaf(sv[v + 1], c, neg_m))};
+          h[e2] = __builtin_convertvector(pf, T2);
+          if constexpr (kSplitP) {
+            psum += pf[0] + pf[1];
+            lo[e2] = __builtin_convertvector(pf - __builtin_convertvector(h[e2], F2), T2);
+          } else {
+            // The denominator sums the rounded P that P.V uses: one v_dot2 per pair.
+            psum = __builtin_amdgcn_fdot2(h[e2], T2{T(1), T(1)}, psum, false);
+          }
+        }
+        const T4 a01 = __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3);
+        const T4 a23 = __builtin_shufflevector(h[2], h[3], 0, 1, 2, 3);
+        pk[c0] = __builtin_shufflevector(a01, a23, 0, 1, 2, 3, 4, 5, 6, 7);
+        if constexpr (kSplitP) {
+          const T4 b01 = __builtin_shufflevector(lo[0], lo[1], 0, 1, 2, 3);
+          const T4 b23 = __builtin_shufflevector(lo[2], lo[3], 0, 1, 2, 3);
+          pk_lo[c0] = __builtin_shufflevector(b01, b23, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+      }
+      return psum;
+    };
+    // Lazy rescaling without a maximum on the common path: P is first computed against
+    // the old running maximum. A lane's sum bounds each of its P, so if no lane's sum
+    // exceeds 2^kRescale every P is at most 2^kRescale (exact in fp32, representable in
+    // fp16/bf16) and the tile is done. Otherwise (always on a wave's first tile, whose
+    // m_run is the finite "no maximum" sentinel, and whenever the scores grew by more than
+    // kRescale) the exact maximum is taken, O and l are rescaled, and P is recomputed.
+    float psum = make_p();
+    if (__any(!(psum <= exp2f(kRescale)))) {
+      float mx = fmaxf(s0[0], s1[0]);
+#pragma unroll
+      for (int v = 1; v < 16; ++v) mx = fmaxf(fmaxf(mx, s0[v]), s1[v]);  // v_max3
+      mx = halves_max(mx) * c;
       const float m_new = fmaxf(m_run, mx);
       const float alpha = fast_exp2(m_run - m_new);
       l_run *= alpha;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha;
       m_run = m_new;
-    }
-    const float neg_m = -m_run;
-    const float c = a.scale_log2;
-    float psum = 0.f;
-    V8 pk[4];
-    V8 pk_lo[kSplitP ? 4 : 1];
-    typedef float F2 __attribute__((ext_vector_type(2)));
-    typedef T T2 __attribute__((ext_vector_type(2)));
-    typedef T T4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-    for (int c0 = 0; c0 < 4; ++c0) {
-      const f32x16& sv = (c0 < 2) ? s0 : s1;
-      T2 h[4], lo[4];
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        const int v = 8 * (c0 & 1) + 2 * e2;
-        const F2 pf = {fast_exp2(fmaf(sv[v], c, neg_m)), fast_exp2(fmaf(sv[v + 1], c, neg_m))};
-        psum += pf[0] + pf[1];
-        h[e2] = __builtin_convertvector(pf, T2);
-        if constexpr (kSplitP)
-          lo[e2] = __builtin_convertvector(pf - __builtin_convertvector(h[e2], F2), T2);
-      }
-      const T4 a01 = __builtin_shufflevector(h[0], h[1], 0, 1, 2, 3);
-      const T4 a23 = __builtin_shufflevector(h[2], h[3], 0, 1, 2, 3);
-      pk[c0] = __builtin_shufflevector(a01, a23, 0, 1, 2, 3, 4, 5, 6, 7);
-      if constexpr (kSplitP) {
-        const T4 b01 = __builtin_shufflevector(lo[0], lo[1], 0, 1, 2, 3);
-        const T4 b23 = __builtin_shufflevector(lo[2], lo[3], 0, 1, 2, 3);
-        pk_lo[c0] = __builtin_shufflevector(b01, b23, 0, 1, 2, 3, 4, 5, 6, 7);
-      }
+      psum = make_p();
     }
     l_run += psum;
 
@@ -456,7 +480,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
 template <typename T, int D, int HG>
 static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream) {
   constexpr int QB = kWaves / HG;
-  dim3 grid(static_cast<unsigned>(a.n_qtiles) * a.R, Hkv * a.hchunks);
+  dim3 grid(static_cast<unsigned>(a.n_qtiles) * a.R * Hkv * a.hchunks);
   hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB>), grid, dim3(kWaves * kWave), 0, stream, a);
   return launch_status();
 }
@@ -467,6 +491,7 @@ static int dispatch_hg(PrefillArgs& a, int Hkv, int max_q_len, hipStream_t strea
   a.hchunks = a.group / hg;
   const int bq = 32 * (kWaves / hg);
   a.n_qtiles = (max_q_len + bq - 1) / bq;
+  a.n_kvh = Hkv;
   switch (hg) {
     case 1: return launch_prefill_mfma<T, D, 1>(a, Hkv, stream);
     case 2: return launch_prefill_mfma<T, D, 2>(a, Hkv, stream);
@@ -507,7 +532,7 @@ extern "C" int ts_prefill_varlen(const void* q, const void* k_cache, const void*
                        (reinterpret_cast<uintptr_t>(v_cache) % 16 == 0);
   if ((dtype == TS_F16 || dtype == TS_BF16) && (D == 64 || D == 128) && aligned) {
     PrefillArgs a{q, k_cache, v_cache, out, block_tables, q_starts, q_lens, context_lens,
-                  R, Hq / Hkv, 1, lbs, 1, q_stride_t, q_stride_h, o_stride_t, o_stride_h,
+                  R, Hq / Hkv, 1, lbs, 1, Hkv, q_stride_t, q_stride_h, o_stride_t, o_stride_h,
                   k_stride_slot, k_stride_head, bt_stride, scale * kLog2e};
     if (dtype == TS_F16) {
       return D == 64 ? dispatch_hg<f16, 64>(a, Hkv, max_q_len, st)
