@@ -146,3 +146,14 @@ def test_baseline_config_3(dtype: torch.dtype) -> None:
     lens = prefill_lengths(32, seed=0)
     c = prefill_case([(0, n) for n in lens], 16, 8, 128, 16, dtype, seed=3)
     check(c, run(c))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_both_workgroup_shapes(dtype: torch.dtype) -> None:
+    # The library runs 8-wave workgroups (128 queries x 2 heads, 3-stage ring) when the
+    # launch has at least two of them per CU, else 4-wave ones (64 queries x 2 heads,
+    # 2-stage ring, two per CU). At Qwen3 shapes 4 prompts of up to 2048 tokens make 512
+    # 8-wave workgroups (8-wave shape on 256 CUs); 3 make 384 (4-wave shape).
+    for lens in ([2048, 1999, 1100, 700], [2048, 1500, 64]):
+        c = prefill_case([(0, n) for n in lens], 16, 8, 128, 16, dtype, seed=len(lens))
+        check(c, run(c))

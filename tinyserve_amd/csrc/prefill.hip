@@ -25,6 +25,10 @@
 // deals workgroups to the 8 XCDs round-robin, with 8 kv heads each head's workgroups
 // share one XCD's L2, where its K/V blocks are re-read by every query tile.
 //
+// Two shapes: 8 waves with a 3-stage ring (one workgroup per CU, 98 KB of LDS) and, for
+// launches with too few query tiles to fill the chip that way, 4 waves with a 2-stage
+// ring (66 KB: two workgroups per CU, half the queries per workgroup).
+//
 // MFMA formulation (v_mfma_f32_32x32x16_{f16,bf16}). Scores are computed transposed,
 // S^T[key, query] = K . Q^T, with K as the A operand (one 16-byte LDS read per lane) and
 // Q^T as the B operand (held in registers for the whole kernel). In the 32x32
@@ -95,15 +99,14 @@ struct PrefillArgs {
 };
 
 constexpr int kBN = 64;     // keys per tile
-constexpr int kWaves = 8;   // waves per workgroup
 constexpr int kWin = 512;   // block ids held in LDS
 
-template <int D>
+template <int D, int W>
 struct TileShape {
-  static constexpr int kUPR = D / 8;                // 16-byte units per row
-  static constexpr int kRPI = kWave / kUPR;         // rows one direct-to-LDS instruction fills
-  static constexpr int kIPW = kBN / kRPI / kWaves;  // such instructions per wave per tensor
-  static_assert(kIPW >= 1 && kIPW * kRPI * kWaves == kBN, "D in {64, 128}");
+  static constexpr int kUPR = D / 8;           // 16-byte units per row
+  static constexpr int kRPI = kWave / kUPR;    // rows one direct-to-LDS instruction fills
+  static constexpr int kIPW = kBN / kRPI / W;  // such instructions per wave per tensor
+  static_assert(kIPW >= 1 && kIPW * kRPI * W == kBN, "D in {64, 128}");
 };
 
 // Physical 16-byte unit of data unit u in row `row` of a tile is u ^ swz(row).
@@ -151,18 +154,20 @@ __device__ __forceinline__ void lds_load16(const void* src, TS_LDS void* dst) {
 // signal fences (no instructions) keep the compiler from moving memory accesses across.
 template <int N>
 __device__ __forceinline__ void ring_barrier() {
-  static_assert(N >= 0 && N < 16, "vmcnt field");
-  __builtin_amdgcn_s_waitcnt(0x0070 | N);  // vmcnt N, expcnt 7 (no wait), lgkmcnt 0
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  // vmcnt N (bits 3:0 and 15:14), expcnt 7 (no wait), lgkmcnt 0
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_barrier();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <typename T, int D, int HG, int QB>
+template <typename T, int D, int HG, int QB, int kWaves, int kStages>
 __global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 prefill_mfma_kernel(const PrefillArgs a) {
   using V8 = typename Mfma<T>::V8;
-  using Sh = TileShape<D>;
+  using Sh = TileShape<D, kWaves>;
+  static_assert(kStages == 2 || kStages == 3, "ring of 2 or 3 stages");
   constexpr int UPR = Sh::kUPR, RPI = Sh::kRPI, IPW = Sh::kIPW;
   constexpr int BQ = 32 * QB;
   constexpr int DT = D / 32;  // 32-row output tiles
@@ -175,12 +180,8 @@ prefill_mfma_kernel(const PrefillArgs a) {
   // and P.V takes two MFMAs. fp16's 11 bits meet the tolerance with one.
   constexpr bool kSplitP = std::is_same_v<T, bf16>;
 
-  __shared__ __attribute__((aligned(16))) T k_st0[TILE];
-  __shared__ __attribute__((aligned(16))) T k_st1[TILE];
-  __shared__ __attribute__((aligned(16))) T k_st2[TILE];
-  __shared__ __attribute__((aligned(16))) T v_st0[TILE];
-  __shared__ __attribute__((aligned(16))) T v_st1[TILE];
-  __shared__ __attribute__((aligned(16))) T v_st2[TILE];
+  __shared__ __attribute__((aligned(16))) T k_ring[kStages * TILE];
+  __shared__ __attribute__((aligned(16))) T v_ring[kStages * TILE];
   __shared__ int32_t ids_lds[kWin];
 
   const int tid = threadIdx.x;
@@ -425,37 +426,56 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
   };
 
-  // ---- the ring: tile t lives in stage t % 3 -------------------------------------------------
-  // Before computing tile t a wave waits for its own loads of tile t (the loads of tile
-  // t + 1, if issued, may stay in flight), then the barrier makes every wave's loads of
-  // tile t visible and certifies that all waves finished tile t - 1, whose stage
-  // receives tile t + 2.
-  auto step = [&](const T* k_cur, const T* v_cur, T* k_next2, T* v_next2, int n0) {
-    if (n0 + kBN < key_end) ring_barrier<DMA_PER_TILE>();
-    else ring_barrier<0>();
-    const int n2 = n0 + 2 * kBN;
-    if (n2 < key_end) {
-      if (!in_window(n2)) {  // rare: drain, move the window to the gather's first block
+  // ---- the ring: tile t lives in stage t % kStages --------------------------------------
+  // Before computing tile t a wave waits for its own loads of tile t (with three stages
+  // the loads of tile t + 1, if issued, may stay in flight), then the barrier makes every
+  // wave's loads of tile t visible and certifies that all waves finished tile t - 1,
+  // whose stage receives tile t + kStages - 1. Stage indices are compile-time constants
+  // (the loop is unrolled kStages times), so every LDS address is a base plus an offset.
+  auto step = [&](const T* k_cur, const T* v_cur, T* k_nx, T* v_nx, int n0) {
+    if constexpr (kStages == 3) {
+      if (n0 + kBN < key_end) ring_barrier<DMA_PER_TILE>();
+      else ring_barrier<0>();
+    } else {
+      ring_barrier<0>();
+    }
+    const int nn = n0 + (kStages - 1) * kBN;
+    if (nn < key_end) {
+      if (!in_window(nn)) {  // rare: drain, move the window to the gather's first block
         __builtin_amdgcn_s_waitcnt(0x0070);
         __syncthreads();
-        fill_window(n2 >> lbs);
+        fill_window(nn >> lbs);
         __syncthreads();
       }
-      gather(k_next2, v_next2, n2);
+      gather(k_nx, v_nx, nn);
     }
     if (n0 < wave_key_end) attend(k_cur, v_cur, n0);
   };
+  T* const k0 = k_ring;
+  T* const v0 = v_ring;
+  T* const k1 = k_ring + TILE;
+  T* const v1 = v_ring + TILE;
+  T* const k2 = k_ring + (kStages - 1) * TILE;  // == k1 with two stages (never used)
+  T* const v2 = v_ring + (kStages - 1) * TILE;
 
   fill_window(0);
   __syncthreads();
-  gather(k_st0, v_st0, 0);
-  if (kBN < key_end) gather(k_st1, v_st1, kBN);
-  for (int n0 = 0; n0 < key_end; n0 += 3 * kBN) {
-    step(k_st0, v_st0, k_st2, v_st2, n0);
-    if (n0 + kBN >= key_end) break;
-    step(k_st1, v_st1, k_st0, v_st0, n0 + kBN);
-    if (n0 + 2 * kBN >= key_end) break;
-    step(k_st2, v_st2, k_st1, v_st1, n0 + 2 * kBN);
+  gather(k0, v0, 0);
+  if constexpr (kStages == 3) {
+    if (kBN < key_end) gather(k1, v1, kBN);
+    for (int n0 = 0; n0 < key_end; n0 += 3 * kBN) {
+      step(k0, v0, k2, v2, n0);
+      if (n0 + kBN >= key_end) break;
+      step(k1, v1, k0, v0, n0 + kBN);
+      if (n0 + 2 * kBN >= key_end) break;
+      step(k2, v2, k1, v1, n0 + 2 * kBN);
+    }
+  } else {
+    for (int n0 = 0; n0 < key_end; n0 += 2 * kBN) {
+      step(k0, v0, k1, v1, n0);
+      if (n0 + kBN >= key_end) break;
+      step(k1, v1, k0, v0, n0 + kBN);
+    }
   }
   // No load may still be writing this workgroup's LDS when its waves end.
   __builtin_amdgcn_s_waitcnt(0x0070);
@@ -477,28 +497,44 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
 }
 
-template <typename T, int D, int HG>
+template <typename T, int D, int HG, int W, int S>
 static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream) {
-  constexpr int QB = kWaves / HG;
+  constexpr int QB = W / HG;
   dim3 grid(static_cast<unsigned>(a.n_qtiles) * a.R * Hkv * a.hchunks);
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB>), grid, dim3(kWaves * kWave), 0, stream, a);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S>), grid, dim3(W * kWave), 0, stream, a);
   return launch_status();
+}
+
+// Query tiles of 32 * (W / HG) queries. The 8-wave shape is the faster one per unit of
+// work; the 4-wave shape halves the work per workgroup and fits two workgroups per CU,
+// which wins when the launch has fewer than two 8-wave workgroups per CU (e.g. one
+// 2048-token prompt: 128 workgroups of 8 waves).
+template <typename T, int D, int W, int S>
+static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, hipStream_t stream) {
+  const int hg = a.group < W ? a.group : W;
+  a.hchunks = a.group / hg;
+  const int bq = 32 * (W / hg);
+  a.n_qtiles = (max_q_len + bq - 1) / bq;
+  a.n_kvh = Hkv;
+  switch (hg) {
+    case 1: return launch_prefill_mfma<T, D, 1, W, S>(a, Hkv, stream);
+    case 2: return launch_prefill_mfma<T, D, 2, W, S>(a, Hkv, stream);
+    case 4: return launch_prefill_mfma<T, D, 4, W, S>(a, Hkv, stream);
+    case 8:
+      if constexpr (W >= 8) return launch_prefill_mfma<T, D, 8, W, S>(a, Hkv, stream);
+      return TS_EUNSUPPORTED;
+    default: return TS_EUNSUPPORTED;
+  }
 }
 
 template <typename T, int D>
 static int dispatch_hg(PrefillArgs& a, int Hkv, int max_q_len, hipStream_t stream) {
-  const int hg = a.group < kWaves ? a.group : kWaves;
-  a.hchunks = a.group / hg;
-  const int bq = 32 * (kWaves / hg);
-  a.n_qtiles = (max_q_len + bq - 1) / bq;
-  a.n_kvh = Hkv;
-  switch (hg) {
-    case 1: return launch_prefill_mfma<T, D, 1>(a, Hkv, stream);
-    case 2: return launch_prefill_mfma<T, D, 2>(a, Hkv, stream);
-    case 4: return launch_prefill_mfma<T, D, 4>(a, Hkv, stream);
-    case 8: return launch_prefill_mfma<T, D, 8>(a, Hkv, stream);
-    default: return TS_EUNSUPPORTED;
-  }
+  const int hg8 = a.group < 8 ? a.group : 8;
+  const int64_t wg8 = static_cast<int64_t>((max_q_len + 32 * (8 / hg8) - 1) / (32 * (8 / hg8))) *
+                      a.R * Hkv * (a.group / hg8);
+  if (a.group <= 4 && wg8 < 2 * static_cast<int64_t>(compute_units()))
+    return dispatch_hg_w<T, D, 4, 2>(a, Hkv, max_q_len, stream);
+  return dispatch_hg_w<T, D, 8, 3>(a, Hkv, max_q_len, stream);
 }
 
 int prefill_rows_generic(const void* q, const void* k, const void* v, void* out,
