@@ -193,6 +193,48 @@ def extra_measurements() -> dict:
         "rms_norm_rows_us": round(ms_r * 1e3, 2), "rms_GB/s": round(b_r / ms_r / 1e6, 1),
         "qk_norm_rope_store_us": round(ms_q * 1e3, 2), "qk_GB/s": round(b_q / ms_q / 1e6, 1),
         "bytes": b_r + b_q}  # fmt: skip
+    # Config 5: the 28-layer decode step.
+    res["decode_step_28l_b64"] = decode_step_28l()
+    return res
+
+
+def decode_step_28l(batch: int = 64, steps: int = 20, seed: int = 5) -> dict:
+    """one decode step of all 28 layers of a random-init
+    Qwen3-0.6B-shaped model (fp16), B=64, contexts ~ U[1024, 4096], 16-token blocks
+    scattered over the pool, replayed as a captured graph. Reported for the reference's
+    16 splits and for this library's split policy: tokens/s and the decode-attention
+    share of the step (a graph of the step's 28 attention launches alone, timed the
+    same way)."""
+    from tinyserve_amd.decode_step import (DecodeGraph, DecodeStep, KVPool, ModelShape,
+                                           random_context_tables, random_weights)  # fmt: skip
+    from tinyserve_amd.step_inputs import DecodeInputs, PagedTable, fill_decode_inputs
+
+    dev = torch.device("cuda:0")
+    shape = ModelShape()
+    w = random_weights(shape, torch.float16, dev, seed)
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1024, 4097, (batch,), generator=g).tolist()
+    blocks, nb = random_context_tables(lens, BS, seed=seed)
+    pool = KVPool(shape, nb, BS, torch.float16, dev)
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    pool.k.normal_(generator=gd)
+    pool.v.normal_(generator=gd)
+    tables = [PagedTable(b, BS, n) for b, n in zip(blocks, lens)]
+    inp = DecodeInputs.empty(batch, max(len(b) for b in blocks), dev)
+    fill_decode_inputs(inp, [(i % shape.vocab, t) for i, t in enumerate(tables)], pool.pad_block)
+    kv_bytes = sum(lens) * shape.num_layers * 2 * shape.kv_size * 2
+    res: dict = {"batch": batch, "ctx_mean": round(sum(lens) / batch, 1), "kv_read_GB": round(kv_bytes / 1e9, 2)}
+    for splits in (16, None):
+        step = DecodeStep(shape, w, pool, splits)
+        full = DecodeGraph(step.forward, inp)
+        attn = DecodeGraph(step.attention_only, inp)
+        ms_step = loop_ms(full.replay, steps, 3)
+        ms_attn = loop_ms(attn.replay, steps, 3)
+        used = splits or num_splits_for(batch, shape.num_kv_heads, inp.block_tables.shape[1])
+        res[f"splits_{used}"] = {"ms_per_step": round(ms_step, 3), "tok_per_s": round(batch / ms_step * 1e3, 1),
+                                 "attention_ms": round(ms_attn, 3), "attention_share": round(ms_attn / ms_step, 3),
+                                 "attention_GB/s": round(kv_bytes / ms_attn / 1e6, 1)}  # fmt: skip
+        del full, attn
     return res
 
 

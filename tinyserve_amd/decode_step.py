@@ -1,0 +1,224 @@
+"""A Qwen3-0.6B-shaped decode step for many sequences through the HIP kernels: the
+reference's ``Qwen3.forward_decode`` with its fused kernels and a kernel decode
+(src/tinyserve/model.py:137-179, 332-356), and a captured graph of it like the
+reference's ``DecodeGraphs`` (src/tinyserve/cuda_graphs.py:135-173).
+
+Per layer, on the flat ``[N]`` rows of a ``DecodeInputs`` (step_inputs.py):
+
+    h    = rms_norm_rows(x, input_layernorm)                       HIP  (fused.hip)
+    qkv  = h @ W_qkv^T                                             GEMM (hipBLASLt via torch)
+    q    = qk_norm_rope_store(q, k, v, ...) -> K/V cache at slots  HIP  (fused.hip)
+    attn = paged decode attention over the block tables            HIP  (decode.hip)
+    x   += attn @ W_o^T
+    h    = rms_norm_rows(x, post_attention_layernorm)              HIP
+    x   += (silu(gate) * up) @ W_down^T, [gate | up] = h @ W_gate_up^T
+
+then the final norm and the tied output head (``[vocab, hidden]``), padded to 8 rows as
+the reference pads it (model.py:214-221). The GEMMs and the SiLU product are library
+work outside the attention hot path; everything on the path is a HIP kernel.
+
+Weights are random (no checkpoints here): linear weights ~ N(0, 0.02) in the model dtype,
+norm weights 1 + 0.1 N(0, 1). The KV pool has the reference's layout (kv_cache.py:20-50):
+per layer ``[num_blocks * block_size + block_size, Hkv, D]``, the last block being the
+padding block that padding rows write and read.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from tinyserve_amd import hip_attention, hip_fused
+from tinyserve_amd.step_inputs import DecodeInputs
+
+HEAD_MIN_ROWS = 8  # the output head runs on at least this many rows (model.py:64)
+
+
+@dataclass(frozen=True)
+class ModelShape:
+    """Qwen3-0.6B by default (config.py of the reference)."""
+
+    hidden: int = 1024
+    num_heads: int = 16
+    num_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 3072
+    vocab: int = 151936
+    num_layers: int = 28
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+
+    @property
+    def q_size(self) -> int:
+        return self.num_heads * self.head_dim
+
+    @property
+    def kv_size(self) -> int:
+        return self.num_kv_heads * self.head_dim
+
+
+def random_weights(shape: ModelShape, dtype: torch.dtype = torch.float16,
+                   device: torch.device | str = "cuda", seed: int = 0) -> dict[str, torch.Tensor]:  # fmt: skip
+    """Random weights under the reference's names, q/k/v and gate/up already merged
+    (model.py:94-127, ``merge_projections``)."""
+    device = torch.device(device)
+    g = torch.Generator(device=device).manual_seed(seed)  # drawn where the weights live
+
+    def lin(rows: int, cols: int) -> torch.Tensor:
+        return (torch.randn(rows, cols, generator=g, device=device) * 0.02).to(dtype)
+
+    def norm(n: int) -> torch.Tensor:
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device=device)).to(dtype)
+
+    s = shape
+    w = {"model.embed_tokens.weight": lin(s.vocab, s.hidden), "model.norm.weight": norm(s.hidden)}
+    for i in range(s.num_layers):
+        p = f"model.layers.{i}."
+        w[p + "input_layernorm.weight"] = norm(s.hidden)
+        w[p + "post_attention_layernorm.weight"] = norm(s.hidden)
+        w[p + "self_attn.qkv_proj.weight"] = lin(s.q_size + 2 * s.kv_size, s.hidden)
+        w[p + "self_attn.o_proj.weight"] = lin(s.hidden, s.q_size)
+        w[p + "self_attn.q_norm.weight"] = norm(s.head_dim)
+        w[p + "self_attn.k_norm.weight"] = norm(s.head_dim)
+        w[p + "mlp.gate_up_proj.weight"] = lin(2 * s.intermediate, s.hidden)
+        w[p + "mlp.down_proj.weight"] = lin(s.hidden, s.intermediate)
+    return w
+
+
+class KVPool:
+    """The KV cache tensors (kv_cache.py:20-50): ``k``, ``v`` of shape
+    ``[L, num_blocks * block_size + block_size, Hkv, D]``; block ``num_blocks`` is the
+    padding block."""
+
+    def __init__(self, shape: ModelShape, num_blocks: int, block_size: int,
+                 dtype: torch.dtype = torch.float16, device: torch.device | str = "cuda") -> None:  # fmt: skip
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.num_slots = num_blocks * block_size
+        self.pad_block = num_blocks
+        dims = (shape.num_layers, self.num_slots + block_size, shape.num_kv_heads, shape.head_dim)
+        self.k = torch.zeros(dims, dtype=dtype, device=device)
+        self.v = torch.zeros(dims, dtype=dtype, device=device)
+
+    @property
+    def memory_bytes(self) -> int:
+        return 2 * self.k.numel() * self.k.element_size()
+
+
+def rope_tables(head_dim: int, theta: float, positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``[T, D]`` float32 cos / sin on the positions' device, angles in float64 (the
+    reference's ``rope_cos_sin``, layers.py:41-65; positions reach 40960)."""
+    inv_freq = theta ** (-torch.arange(0, head_dim, 2, dtype=torch.float64, device=positions.device) / head_dim)
+    ang = positions.to(torch.float64)[:, None] * inv_freq[None, :]
+    ang = torch.cat([ang, ang], dim=-1)
+    return ang.cos().float(), ang.sin().float()
+
+
+class DecodeStep:
+    """``forward(inputs)`` -> ``[N, vocab]`` float32 logits, writing each row's new k/v
+    into the pool (the reference's ``forward_decode``). Nothing in it waits for the GPU,
+    so a graph can capture it.
+
+    ``num_splits``: the decode kernel's split count (None: the launcher's policy; the
+    reference's config-5 step forces 16)."""
+
+    def __init__(self, shape: ModelShape, weights: dict[str, torch.Tensor], pool: KVPool,
+                 num_splits: int | None = None) -> None:  # fmt: skip
+        self.shape = shape
+        self.w = weights
+        self.pool = pool
+        self.num_splits = num_splits
+        self.scale = shape.head_dim**-0.5
+
+    def _attention(self, i: int, q: torch.Tensor, inputs: DecodeInputs) -> torch.Tensor:
+        return hip_attention.launch_paged_decode_split(
+            q, self.pool.k[i], self.pool.v[i], inputs.block_tables, inputs.context_lens,
+            self.scale, self.pool.block_size, self.num_splits)  # fmt: skip
+
+    def layer(self, i: int, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+              inputs: DecodeInputs) -> torch.Tensor:  # fmt: skip
+        s, w, p = self.shape, self.w, f"model.layers.{i}."
+        n = x.shape[0]
+        h = hip_fused.rms_norm_rows(x, w[p + "input_layernorm.weight"], s.rms_norm_eps)
+        qkv = F.linear(h, w[p + "self_attn.qkv_proj.weight"])
+        q, k, v = torch.split(qkv, [s.q_size, s.kv_size, s.kv_size], dim=1)
+        q = hip_fused.qk_norm_rope_store(
+            q.view(n, s.num_heads, s.head_dim), k.view(n, s.num_kv_heads, s.head_dim),
+            v.view(n, s.num_kv_heads, s.head_dim), w[p + "self_attn.q_norm.weight"],
+            w[p + "self_attn.k_norm.weight"], cos, sin, inputs.slots, self.pool.k[i],
+            self.pool.v[i], s.rms_norm_eps)  # fmt: skip
+        attn = self._attention(i, q, inputs)
+        x = x + F.linear(attn.reshape(n, s.q_size), w[p + "self_attn.o_proj.weight"])
+        h = hip_fused.rms_norm_rows(x, w[p + "post_attention_layernorm.weight"], s.rms_norm_eps)
+        gate, up = F.linear(h, w[p + "mlp.gate_up_proj.weight"]).chunk(2, dim=1)
+        return x + F.linear(F.silu(gate) * up, w[p + "mlp.down_proj.weight"])
+
+    def forward(self, inputs: DecodeInputs) -> torch.Tensor:
+        s = self.shape
+        cos, sin = rope_tables(s.head_dim, s.rope_theta, inputs.positions)
+        x = self.w["model.embed_tokens.weight"][inputs.token_ids]
+        for i in range(s.num_layers):
+            x = self.layer(i, x, cos, sin, inputs)
+        x = hip_fused.rms_norm_rows(x, self.w["model.norm.weight"], s.rms_norm_eps)
+        n = x.shape[0]
+        if n < HEAD_MIN_ROWS:
+            x = F.pad(x, (0, 0, 0, HEAD_MIN_ROWS - n))
+        return F.linear(x, self.w["model.embed_tokens.weight"])[:n].float()
+
+    def attention_only(self, inputs: DecodeInputs) -> torch.Tensor:
+        """The step's decode-attention launches alone (one per layer, on the current
+        cache contents and a fixed q): for measuring the attention share of a step."""
+        s = self.shape
+        q = torch.zeros(inputs.num_rows, s.num_heads, s.head_dim, dtype=self.pool.k.dtype,
+                        device=self.pool.k.device)  # fmt: skip
+        out = q
+        for i in range(s.num_layers):
+            out = self._attention(i, q, inputs)
+        return out
+
+
+class DecodeGraph:
+    """One captured graph of ``fn(inputs)`` on fixed ``inputs`` buffers (the reference's
+    ``DecodeGraphs`` for one bucket, cuda_graphs.py:135-173): ``replay()`` re-runs it on
+    whatever the buffers hold and returns the output buffer (overwritten by the next
+    replay). The pass runs twice on a side stream first, so every library handle and
+    kernel is loaded before capture."""
+
+    def __init__(self, fn, inputs: DecodeInputs) -> None:  # noqa: ANN001
+        dev = inputs.token_ids.device
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                fn(inputs)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize(dev)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.output = fn(inputs)
+        torch.cuda.synchronize(dev)
+
+    def replay(self) -> torch.Tensor:
+        self.graph.replay()
+        return self.output
+
+
+def random_context_tables(lens: list[int], block_size: int, num_blocks: int | None = None,
+                          seed: int = 0) -> tuple[list[list[int]], int]:  # fmt: skip
+    """Block lists for sequences of ``lens`` tokens, scattered over a pool by a seeded
+    permutation (the synthetic input of the config-5 step). Returns the lists and the
+    pool's block count."""
+    need = [math.ceil(n / block_size) for n in lens]
+    total = sum(need)
+    num_blocks = num_blocks or total
+    if num_blocks < total:
+        raise ValueError(f"{total} blocks needed, the pool has {num_blocks}")
+    perm = torch.randperm(num_blocks, generator=torch.Generator().manual_seed(seed)).tolist()
+    out, at = [], 0
+    for k in need:
+        out.append(perm[at : at + k])
+        at += k
+    return out, num_blocks
