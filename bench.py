@@ -156,6 +156,33 @@ def cpu_baseline(case, splits: int, budget_s: float = 15.0) -> dict:
                       f"{int(lens[0])} fp16 workload, {reps} rep(s), {dt:.2f} s each"}  # fmt: skip
 
 
+def batched_sdpa_prefill(p, out: torch.Tensor) -> torch.Tensor:
+    """The reference's batched prefill path on the GPU (attention.py:144-220): all
+    sequences' queries and keys gathered into one padded rectangle, one masked
+    scaled-dot-product call in float32 as the reference computes it. A timing
+    comparison for the prefill kernel (its T4 default path), built once per call like
+    the reference's ``prefill_plan`` + ``batched_prefill_attention``."""
+    lens, totals, starts = p.q_lens.tolist(), p.ctx_lens.tolist(), p.starts.tolist()
+    dev = p.q.device
+    lq, lk, bs = max(lens), max(totals), p.block_size
+    i = torch.arange(lq, device=dev)
+    n = torch.tensor(lens, device=dev)[:, None]
+    rows = torch.tensor(starts, device=dev)[:, None] + torch.minimum(i[None, :], n - 1)
+    j = torch.arange(lk, device=dev)
+    slots = p.tables.long()[:, (j // bs).clamp(max=p.tables.shape[1] - 1)] * bs + j % bs
+    q_pos = torch.tensor(totals, device=dev)[:, None] - n + torch.minimum(i[None, :], n - 1)
+    mask = (j[None, None, :] <= q_pos[:, :, None])[:, None]
+    group = p.q.shape[1] // p.k.shape[1]
+    qb = p.q[rows].float().transpose(1, 2)
+    kb = p.k[slots].float().repeat_interleave(group, dim=2).transpose(1, 2)
+    vb = p.v[slots].float().repeat_interleave(group, dim=2).transpose(1, 2)
+    ob = torch.nn.functional.scaled_dot_product_attention(qb, kb, vb, attn_mask=mask, scale=p.scale)
+    ob = ob.transpose(1, 2).to(p.q.dtype)
+    for r, (st, ln) in enumerate(zip(starts, lens)):
+        out[st : st + ln] = ob[r, :ln]
+    return out
+
+
 def extra_measurements() -> dict:
     dev = torch.device("cuda:0")
     res: dict = {}
@@ -176,6 +203,14 @@ def extra_measurements() -> dict:
         res[f"prefill_varlen32_{str(dt).split('.')[-1]}"] = {
             "ms": round(ms, 4), "TFLOP/s": round(tf, 1), "mfma_frac": round(tf / FP16_PEAK_TFLOPS, 4),
             "flops": flops}  # fmt: skip
+        if dt == torch.float16:  # the reference's batched SDPA path on the same input
+            ref_out = torch.empty_like(p.q)
+            ms_ref = loop_ms(lambda: batched_sdpa_prefill(p, ref_out), 5, 1)
+            diff = (ref_out.float() - out.float()).abs().max()  # `out` holds the HIP result
+            res["prefill_varlen32_reference_batched_sdpa_fp32"] = {
+                "ms": round(ms_ref, 3), "TFLOP/s": round(flops / ms_ref / 1e9, 1),
+                "hip_kernel_speedup": round(ms_ref / ms, 1),
+                "max_abs_diff_vs_hip": float(diff)}  # fmt: skip
     one = prefill_case([(0, 2048)], HQ, HKV, D, BS, torch.float16, sentinel=False, device=dev)
     out = torch.empty_like(one.q)
     ms = loop_ms(lambda: paged_prefill_attention(*one.args(), out=out), 20, 3)

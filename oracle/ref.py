@@ -9,6 +9,7 @@ Each function follows one reference function (paths relative to the reference re
     attend_paged        src/tinyserve/attention.py:62-111    paged_gqa_attention
     decode_ref          src/tinyserve/attention.py:114-141   paged_decode_attention_ref
     prefill_ref         tests/test_triton_prefill.py:57-61   paged_gqa_attention per sequence
+    batched_prefill_ref src/tinyserve/attention.py:144-220   prefill_plan + batched SDPA
     rms_norm            src/tinyserve/layers.py:14-38
     rope_cos_sin        src/tinyserve/layers.py:41-65        (angles in float64)
     apply_rope          src/tinyserve/layers.py:68-91
@@ -117,6 +118,48 @@ def prefill_ref(
     for r, (s, n, total) in enumerate(zip(q_starts.tolist(), q_lens.tolist(), context_lens.tolist())):
         slots = block_slots(block_tables[r], total, block_size)
         out[s : s + n] = attend_paged(q[s : s + n], k_cache, v_cache, slots, scale)
+    return out
+
+
+def batched_prefill_ref(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    q_starts: torch.Tensor,
+    q_lens: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The reference's batched prefill path (attention.py:144-220, ``prefill_plan`` +
+    ``batched_prefill_attention``): every sequence's queries and keys gathered into one
+    padded rectangle and attended by a single masked scaled-dot-product call in float32.
+    Padded query rows repeat the sequence's last query (their results are dropped);
+    padded keys are masked out by causality. A second, independently structured oracle
+    for ``prefill_ref``; rows of no sequence are left as in ``out``."""
+    out = torch.empty_like(q) if out is None else out
+    starts, lens, totals = q_starts.tolist(), q_lens.tolist(), context_lens.tolist()
+    if not lens:
+        return out
+    lq, lk = max(lens), max(totals)
+    i = torch.arange(lq)
+    rows = torch.stack([s + torch.clamp(i, max=n - 1) for s, n in zip(starts, lens)])  # [R, Lq]
+    slots = torch.zeros((len(lens), lk), dtype=torch.int64)
+    for r, total in enumerate(totals):
+        slots[r, :total] = block_slots(block_tables[r], total, block_size)
+    first = torch.tensor([t - n for t, n in zip(totals, lens)])[:, None]  # position of query 0
+    q_pos = first + torch.clamp(i[None, :], max=torch.tensor(lens)[:, None] - 1)
+    mask = torch.arange(lk)[None, None, :] <= q_pos[:, :, None]  # [R, Lq, Lk]
+    group = q.shape[1] // k_cache.shape[1]
+    qb = q[rows].float().transpose(1, 2)  # [R, Hq, Lq, D]
+    kb = k_cache[slots].float().repeat_interleave(group, dim=2).transpose(1, 2)
+    vb = v_cache[slots].float().repeat_interleave(group, dim=2).transpose(1, 2)
+    ob = torch.nn.functional.scaled_dot_product_attention(qb, kb, vb, attn_mask=mask[:, None], scale=scale)
+    ob = ob.transpose(1, 2).to(q.dtype)  # [R, Lq, Hq, D]
+    for r, (s, n) in enumerate(zip(starts, lens)):
+        out[s : s + n] = ob[r, :n]
     return out
 
 

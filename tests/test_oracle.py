@@ -223,3 +223,32 @@ def test_kv_write_places_exactly_and_touches_nothing_else() -> None:
     others = torch.ones(16, dtype=torch.bool)
     others[slots] = False
     assert kc[others].isnan().all() and vc[others].isnan().all()
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_batched_prefill_equals_per_sequence_prefill(seed: int) -> None:
+    # The reference's two prefill paths agree (test_batched_forward.py's premise): one
+    # padded masked SDPA call over all sequences == paged_gqa_attention one at a time,
+    # including chunked-prefill sequences (context longer than the new rows) and a gap
+    # row that belongs to no sequence.
+    g = torch.Generator().manual_seed(seed)
+    specs = [(0, 5), (7, 3), (0, 1), (12, 9)]  # (cached, new)
+    bs, hq, hkv, d = 4, 4, 2, 8
+    nblk = [-(-(c + n) // bs) for c, n in specs]
+    perm = torch.randperm(sum(nblk) + 2, generator=g).tolist()
+    tables = torch.zeros((len(specs), max(nblk)), dtype=torch.int32)
+    at = 0
+    for r, k in enumerate(nblk):
+        tables[r, :k] = torch.tensor(perm[at : at + k])
+        at += k
+    kc = torch.randn((sum(nblk) + 2) * bs, hkv, d, generator=g)
+    vc = torch.randn((sum(nblk) + 2) * bs, hkv, d, generator=g)
+    lens = [n for _, n in specs]
+    starts = torch.tensor([sum(lens[:r]) + r for r in range(len(lens))], dtype=torch.int32)  # gaps
+    q = torch.randn(int(starts[-1]) + lens[-1] + 1, hq, d, generator=g)
+    ql = torch.tensor(lens, dtype=torch.int32)
+    ctx = torch.tensor([c + n for c, n in specs], dtype=torch.int32)
+    a = ref.prefill_ref(q, kc, vc, tables, starts, ql, ctx, 0.35, bs, torch.full_like(q, 7.0))
+    b = ref.batched_prefill_ref(q, kc, vc, tables, starts, ql, ctx, 0.35, bs, torch.full_like(q, 7.0))
+    torch.testing.assert_close(b, a, atol=1e-5, rtol=1e-5)
+    assert (b[5] == 7.0).all()  # the gap row after sequence 0 is untouched
