@@ -11,7 +11,7 @@
 // lanes of a token reads LPT * 16 contiguous bytes. A wave therefore streams
 // TPW = 64 / LPT tokens per iteration (16 tokens of a 16-slot block for fp16 D=128:
 // 4 KB of K and 4 KB of V per wave per iteration, both issued before the previous
-// iteration's math so that two iterations are always in flight).
+// iteration's math so that three iterations are always in flight).
 //
 // Waves per workgroup. A decode launch gives each (sequence, head tile, split) a
 // workgroup of W = 1, 2 or 4 waves; wave w takes the w-th of W contiguous block ranges of
@@ -33,7 +33,7 @@
 #define TS_DECODE_LANE_BYTES 64
 #endif
 #ifndef TS_DECODE_NBUF
-#define TS_DECODE_NBUF 2
+#define TS_DECODE_NBUF 3
 #endif
 #ifndef TS_DECODE_WAVES_PER_EU
 #define TS_DECODE_WAVES_PER_EU 1
@@ -209,7 +209,10 @@ void paged_attend_kernel(const AttendArgs a) {
   const int wave = PREFILL ? 0 : threadIdx.x / kWave;
   const int c = lane % LPT;
   const int tl = lane / LPT;
-  const int h0 = blockIdx.y * HT;
+  // Decode grid (head tiles, sequences, splits): the head tiles of one sequence are
+  // dispatched together, so the kv heads of a slot (one contiguous 2 KB row at Qwen3
+  // shapes) are read at about the same time. Prefill grid (rows, head tiles).
+  const int h0 = (PREFILL ? blockIdx.y : blockIdx.x) * HT;
   const int kvh = h0 / a.group;
 
   int seq, ctx, split = 0;
@@ -224,7 +227,7 @@ void paged_attend_kernel(const AttendArgs a) {
     qrow = row * a.q_sb;
     orow = row * a.o_sb;
   } else {
-    seq = blockIdx.x;
+    seq = blockIdx.y;
     split = blockIdx.z;
     ctx = a.lens[seq];
     qrow = seq * a.q_sb;
@@ -484,6 +487,7 @@ extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || splits < 1 || !is_pow2(block_size))
     return TS_EINVAL;
   if (B == 0) return 0;
+  if (B > 65535) return TS_EUNSUPPORTED;  // sequences are the grid's y dimension
   if (splits > 1 && (!m || !l || !acc)) return TS_EINVAL;
   if (splits == 1 && !out) return TS_EINVAL;
   const int group = Hq / Hkv;
@@ -497,7 +501,7 @@ extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v
                nullptr, Hq, group, ilog2(block_size), splits, wpg, 0, q_stride_b, q_stride_h,
                o_stride_b, o_stride_h, k_stride_slot, k_stride_head, bt_stride,
                scale * kLog2e};
-  dim3 grid(B, Hq / ht, splits);
+  dim3 grid(Hq / ht, B, splits);
   return dispatch_attend<false>(a, dtype, D, ht, grid, static_cast<hipStream_t>(stream));
 }
 

@@ -98,15 +98,14 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-constexpr int kBN = 64;     // keys per tile
 constexpr int kWin = 512;   // block ids held in LDS
 
-template <int D, int W>
+template <int D, int W, int BN>
 struct TileShape {
-  static constexpr int kUPR = D / 8;           // 16-byte units per row
-  static constexpr int kRPI = kWave / kUPR;    // rows one direct-to-LDS instruction fills
-  static constexpr int kIPW = kBN / kRPI / W;  // such instructions per wave per tensor
-  static_assert(kIPW >= 1 && kIPW * kRPI * W == kBN, "D in {64, 128}");
+  static constexpr int kUPR = D / 8;          // 16-byte units per row
+  static constexpr int kRPI = kWave / kUPR;   // rows one direct-to-LDS instruction fills
+  static constexpr int kIPW = BN / kRPI / W;  // such instructions per wave per tensor
+  static_assert(kIPW >= 1 && kIPW * kRPI * W == BN, "D in {64, 128}");
 };
 
 // Physical 16-byte unit of data unit u in row `row` of a tile is u ^ swz(row).
@@ -162,11 +161,13 @@ __device__ __forceinline__ void ring_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <typename T, int D, int HG, int QB, int kWaves, int kStages>
+template <typename T, int D, int HG, int QB, int kWaves, int kStages, int kBN>
 __global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 prefill_mfma_kernel(const PrefillArgs a) {
   using V8 = typename Mfma<T>::V8;
-  using Sh = TileShape<D, kWaves>;
+  using Sh = TileShape<D, kWaves, kBN>;
+  constexpr int NH = kBN / 32;  // 32-key halves of S^T (one MFMA accumulator each)
+  constexpr int NC = kBN / 16;  // 16-key chunks of P^T (one PV B operand each)
   static_assert(kStages == 2 || kStages == 3, "ring of 2 or 3 stages");
   constexpr int UPR = Sh::kUPR, RPI = Sh::kRPI, IPW = Sh::kIPW;
   constexpr int BQ = 32 * QB;
@@ -294,50 +295,50 @@ prefill_mfma_kernel(const PrefillArgs a) {
   const int vswz = v_swz<D>(vkey_lane);           // key & 3 = vj >> 2 for every read
 
   auto attend = [&](const T* k_lds, const T* v_lds, int n0) {
-    // S^T = K . Q^T for the tile's two 32-key halves: two independent MFMA chains.
-    // The K operands of chunk kc + 1 are read while chunk kc multiplies.
-    f32x16 s0 = {}, s1 = {};
+    // S^T = K . Q^T for the tile's 32-key parts: NH independent MFMA chains. The K
+    // operands of chunk kc + 1 are read while chunk kc multiplies.
+    f32x16 s[NH];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) s[h] = f32x16{};
     {
       const T* kr0 = k_lds + col * D;
-      const T* kr1 = kr0 + 32 * D;
-      auto kread = [&](int kc, V8& x0, V8& x1) {
+      auto kread = [&](int kc, V8 (&x)[NH]) {
         const int u = ((2 * kc + half) ^ kphys) * 8;
-        x0 = *reinterpret_cast<const V8*>(kr0 + u);
-        x1 = *reinterpret_cast<const V8*>(kr1 + u);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) x[h] = *reinterpret_cast<const V8*>(kr0 + 32 * h * D + u);
       };
-      V8 ka[2][2];
-      kread(0, ka[0][0], ka[0][1]);
+      V8 ka[2][NH];
+      kread(0, ka[0]);
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        if (kc + 1 < KC) kread(kc + 1, ka[(kc + 1) & 1][0], ka[(kc + 1) & 1][1]);
-        s0 = Mfma<T>::mma(ka[kc & 1][0], qreg[kc], s0);
-        s1 = Mfma<T>::mma(ka[kc & 1][1], qreg[kc], s1);
+        if (kc + 1 < KC) kread(kc + 1, ka[(kc + 1) & 1]);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) s[h] = Mfma<T>::mma(ka[kc & 1][h], qreg[kc], s[h]);
       }
       // Keep that order through scheduling: reads of chunk kc + 1, then MFMAs of kc.
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, NH, 0);
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
-        if (kc + 1 < KC) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+        if (kc + 1 < KC) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, NH, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, NH, 0);
       }
     }
-    // Causal mask, only on a tile that crosses this wave's diagonal: item v of the lane
-    // holds key n0 + 8 (v / 4) + 4 half + v % 4 (+ 32 in s1).
+    // Causal mask, only on a tile that crosses this wave's diagonal: item v of part h
+    // holds key n0 + 32 h + 8 (v / 4) + 4 half + v % 4.
     if (n0 + kBN - 1 > wave_pos_min) {
       const int lim = pos - n0 - 4 * half;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int kofs = 8 * (v >> 2) + (v & 3);
-        if (kofs > lim) s0[v] = -INFINITY;
-        if (kofs + 32 > lim) s1[v] = -INFINITY;
-      }
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (32 * h + 8 * (v >> 2) + (v & 3) > lim) s[h][v] = -INFINITY;
     }
 
     // Online softmax for this lane's query, in base 2 with the scale folded into one
     // FMA: p = 2^(s * c - m), c = scale * log2(e) > 0.
     const float c = a.scale_log2;
-    V8 pk[4];
-    V8 pk_lo[kSplitP ? 4 : 1];
+    V8 pk[NC];
+    V8 pk_lo[kSplitP ? NC : 1];
     typedef float F2 __attribute__((ext_vector_type(2)));
     typedef T T2 __attribute__((ext_vector_type(2)));
     typedef T T4 __attribute__((ext_vector_type(4)));
@@ -346,8 +347,8 @@ prefill_mfma_kernel(const PrefillArgs a) {
       const float neg_m = -m_run;
       float psum = 0.f;
 #pragma unroll
-      for (int c0 = 0; c0 < 4; ++c0) {
-        const f32x16& sv = (c0 < 2) ? s0 : s1;
+      for (int c0 = 0; c0 < NC; ++c0) {
+        const f32x16& sv = s[c0 >> 1];
         T2 h[4], lo[4];
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
@@ -381,9 +382,11 @@ prefill_mfma_kernel(const PrefillArgs a) {
     // kRescale) the exact maximum is taken, O and l are rescaled, and P is recomputed.
     float psum = make_p();
     if (__any(!(psum <= exp2f(kRescale)))) {
-      float mx = fmaxf(s0[0], s1[0]);
+      float mx = s[0][0];
 #pragma unroll
-      for (int v = 1; v < 16; ++v) mx = fmaxf(fmaxf(mx, s0[v]), s1[v]);  // v_max3
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int v = (h == 0 ? 1 : 0); v < 16; ++v) mx = fmaxf(mx, s[h][v]);
       mx = halves_max(mx) * c;
       const float m_new = fmaxf(m_run, mx);
       const float alpha = fast_exp2(m_run - m_new);
@@ -398,7 +401,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
     // O^T += V^T . P^T, the V^T operand by two transposing reads per MFMA; the operand
     // of step i + 1 is read while step i multiplies (step i = (dt, c0), c0 fastest).
     auto vread = [&](int i) -> V8 {
-      const int dt = i >> 2, c0 = i & 3;
+      const int dt = i / NC, c0 = i % NC;
       const int d = dt * 32 + vd_lane;
       s16x4 part[2];
 #pragma unroll
@@ -412,16 +415,16 @@ prefill_mfma_kernel(const PrefillArgs a) {
     V8 va[2];
     va[0] = vread(0);
 #pragma unroll
-    for (int i = 0; i < 4 * DT; ++i) {
-      if (i + 1 < 4 * DT) va[(i + 1) & 1] = vread(i + 1);
-      const int dt = i >> 2, c0 = i & 3;
+    for (int i = 0; i < NC * DT; ++i) {
+      if (i + 1 < NC * DT) va[(i + 1) & 1] = vread(i + 1);
+      const int dt = i / NC, c0 = i % NC;
       oacc[dt] = Mfma<T>::mma(va[i & 1], pk[c0], oacc[dt]);
       if constexpr (kSplitP) oacc[dt] = Mfma<T>::mma(va[i & 1], pk_lo[c0], oacc[dt]);
     }
     __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
 #pragma unroll
-    for (int i = 0; i < 4 * DT; ++i) {
-      if (i + 1 < 4 * DT) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
+    for (int i = 0; i < NC * DT; ++i) {
+      if (i + 1 < NC * DT) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 1);
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, kSplitP ? 2 : 1, 1);
     }
   };
@@ -497,11 +500,11 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
 }
 
-template <typename T, int D, int HG, int W, int S>
+template <typename T, int D, int HG, int W, int S, int BN>
 static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream) {
   constexpr int QB = W / HG;
   dim3 grid(static_cast<unsigned>(a.n_qtiles) * a.R * Hkv * a.hchunks);
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S>), grid, dim3(W * kWave), 0, stream, a);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN>), grid, dim3(W * kWave), 0, stream, a);
   return launch_status();
 }
 
@@ -509,7 +512,7 @@ static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream
 // work; the 4-wave shape halves the work per workgroup and fits two workgroups per CU,
 // which wins when the launch has fewer than two 8-wave workgroups per CU (e.g. one
 // 2048-token prompt: 128 workgroups of 8 waves).
-template <typename T, int D, int W, int S>
+template <typename T, int D, int W, int S, int BN>
 static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, hipStream_t stream) {
   const int hg = a.group < W ? a.group : W;
   a.hchunks = a.group / hg;
@@ -517,11 +520,11 @@ static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, hipStream_t str
   a.n_qtiles = (max_q_len + bq - 1) / bq;
   a.n_kvh = Hkv;
   switch (hg) {
-    case 1: return launch_prefill_mfma<T, D, 1, W, S>(a, Hkv, stream);
-    case 2: return launch_prefill_mfma<T, D, 2, W, S>(a, Hkv, stream);
-    case 4: return launch_prefill_mfma<T, D, 4, W, S>(a, Hkv, stream);
+    case 1: return launch_prefill_mfma<T, D, 1, W, S, BN>(a, Hkv, stream);
+    case 2: return launch_prefill_mfma<T, D, 2, W, S, BN>(a, Hkv, stream);
+    case 4: return launch_prefill_mfma<T, D, 4, W, S, BN>(a, Hkv, stream);
     case 8:
-      if constexpr (W >= 8) return launch_prefill_mfma<T, D, 8, W, S>(a, Hkv, stream);
+      if constexpr (W >= 8) return launch_prefill_mfma<T, D, 8, W, S, BN>(a, Hkv, stream);
       return TS_EUNSUPPORTED;
     default: return TS_EUNSUPPORTED;
   }
@@ -533,8 +536,8 @@ static int dispatch_hg(PrefillArgs& a, int Hkv, int max_q_len, hipStream_t strea
   const int64_t wg8 = static_cast<int64_t>((max_q_len + 32 * (8 / hg8) - 1) / (32 * (8 / hg8))) *
                       a.R * Hkv * (a.group / hg8);
   if (a.group <= 4 && wg8 < 2 * static_cast<int64_t>(compute_units()))
-    return dispatch_hg_w<T, D, 4, 2>(a, Hkv, max_q_len, stream);
-  return dispatch_hg_w<T, D, 8, 3>(a, Hkv, max_q_len, stream);
+    return dispatch_hg_w<T, D, 4, 2, 64>(a, Hkv, max_q_len, stream);
+  return dispatch_hg_w<T, D, 8, 3, 64>(a, Hkv, max_q_len, stream);
 }
 
 int prefill_rows_generic(const void* q, const void* k, const void* v, void* out,

@@ -6,7 +6,7 @@ Kernel shape (gfx950). One wave64 per (sequence, query-head tile, split): the gr
 and split launches give a wave the whole GQA group of one kv head (both query heads of
 Qwen3-0.6B), so every K/V byte is read once; the per-query-head launch
 (``paged_decode_attention``, any head grouping) gives it one query head. Each wave
-streams 16-byte K/V vectors of its range of cache blocks, two iterations in flight, and
+streams 16-byte K/V vectors of its range of cache blocks, three iterations in flight, and
 keeps an online softmax per token lane, merged across lanes once at the end. With more
 than one split, every range writes an fp32 partial (m, l, acc) and a second kernel
 combines them (the reference's ``_merge_splits_kernel``, :299-327).
