@@ -186,7 +186,7 @@ def batched_sdpa_prefill(p, out: torch.Tensor) -> torch.Tensor:
 def extra_measurements() -> dict:
     dev = torch.device("cuda:0")
     res: dict = {}
-    # Config 2: decode B=32 x 256, 4 splits, a 4096-block pool.
+    # Config 2: decode B=32 x 256, 4 splits (in-workgroup: one launch), a 4096-block pool.
     c = decode_bench_case(32, 256, pool_blocks=4096, device=dev, seed=1)
     ms = loop_ms(lambda: launch_paged_decode_split(*c.args(), c.scale, BS, num_splits=4), 200, 20)
     nb = decode_bytes(32, 256)["step"]

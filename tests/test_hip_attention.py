@@ -233,3 +233,14 @@ def test_every_workgroup_width_gives_the_reference(batch: int, splits: int) -> N
     out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, num_splits=splits)
     assert torch.isfinite(out).all()
     assert_matches(out, want, torch.float16, f"B={batch} splits={splits}")
+
+
+@pytest.mark.parametrize("splits", [2, 3, 4])
+def test_partials_and_combine_at_small_split_counts(splits: int) -> None:
+    # launch_paged_decode_split runs up to 4 splits inside one workgroup; the C entry's
+    # HBM-partial + combine path at those counts is checked here directly.
+    c = decode_case([17, 300, 33, 1], dtype=torch.float16, seed=splits)
+    want = oracle32(c)
+    g = on_gpu(c)
+    out = ha._launch(*g.args(), g.scale, g.block_size, splits, 0)
+    assert_matches(out, want, torch.float16, f"splits={splits}")
