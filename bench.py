@@ -211,6 +211,13 @@ def extra_measurements() -> dict:
                 "ms": round(ms_ref, 3), "TFLOP/s": round(flops / ms_ref / 1e9, 1),
                 "hip_kernel_speedup": round(ms_ref / ms, 1),
                 "max_abs_diff_vs_hip": float(diff)}  # fmt: skip
+    # 2048-token prompts: a batch of 4 (fills the chip) and one alone (the critical path).
+    four = prefill_case([(0, 2048)] * 4, HQ, HKV, D, BS, torch.float16, sentinel=False, device=dev)
+    out4 = torch.empty_like(four.q)
+    ms = loop_ms(lambda: paged_prefill_attention(*four.args(), out=out4), 20, 3)
+    f4 = 4 * 4 * HQ * D * 2048 * 2049 // 2
+    res["prefill_4x2048_float16"] = {"ms": round(ms, 4), "TFLOP/s": round(f4 / ms / 1e9, 1),
+                                     "mfma_frac": round(f4 / ms / 1e9 / FP16_PEAK_TFLOPS, 4)}
     one = prefill_case([(0, 2048)], HQ, HKV, D, BS, torch.float16, sentinel=False, device=dev)
     out = torch.empty_like(one.q)
     ms = loop_ms(lambda: paged_prefill_attention(*one.args(), out=out), 20, 3)
