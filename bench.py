@@ -290,6 +290,8 @@ def main() -> None:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--profile", choices=["prefill_varlen32"], default=None,
+                    help="only launch one workload 3 times (for a profiler) and print what ran")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run 3 plain device copies of this many MiB (a known-size kernel "
                          "that calibrates the HBM byte counters of a profiler)")
@@ -302,6 +304,16 @@ def main() -> None:
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(2)
     _lib.load()
+    if args.profile == "prefill_varlen32":  # config 3's fp16 prefill, nothing else
+        lens = prefill_lengths(32, seed=0)
+        p = prefill_case([(0, n) for n in lens], HQ, HKV, D, BS, torch.float16, seed=3, sentinel=False,
+                         device=torch.device("cuda:0"))  # fmt: skip
+        out = torch.empty_like(p.q)
+        for _ in range(3):
+            paged_prefill_attention(*p.args(), out=out)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": args.profile, "launches": 3, "sequences": len(lens)}), flush=True)
+        return
     nb = math.ceil(args.ctx / BS)
     splits = args.splits or num_splits_for(args.batch, HKV, nb)
     r = time_decode(args.batch, args.ctx, splits, args.steps, args.warmup)
