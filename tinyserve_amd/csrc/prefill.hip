@@ -294,7 +294,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
   const int vd_lane = 16 * vdsub + 4 * (vj & 3);  // + 32 dt
   const int vswz = v_swz<D>(vkey_lane);           // key & 3 = vj >> 2 for every read
 
-  auto attend = [&](const T* k_lds, const T* v_lds, int n0) {
+  auto attend = [&](const T* k_lds, const T* v_lds, int n0) __attribute__((always_inline)) {
     // S^T = K . Q^T for the tile's 32-key parts: NH independent MFMA chains. The K
     // operands of chunk kc + 1 are read while chunk kc multiplies.
     f32x16 s[NH];
