@@ -1,11 +1,13 @@
 """The decode step through the HIP kernels (``tinyserve_amd.decode_step``) on the GPU.
 
-Mirrors the reference's tests/test_decode_inputs.py:80-130 and tests/test_cuda_graphs.py:
-the step's logits and cache writes against a reference step composed from the oracle
-(``rms_norm``, ``rope_cos_sin``, ``qk_norm_rope_store_ref``, ``decode_ref``) and plain
-fp32 matrix products on the CPU, on a tiny random Qwen3 in fp32; padding rows leave real
-rows unchanged; a captured graph gives the eager result on every replay, with other work
-between replays.
+Mirrors the reference's tests/test_decode_inputs.py:80-130, tests/test_cuda_graphs.py and
+tests/test_batched_forward.py: the step's logits and cache writes against a reference step
+composed from the oracle (``rms_norm``, ``rope_cos_sin``, ``qk_norm_rope_store_ref``,
+``decode_ref`` / ``prefill_ref``) and plain fp32 matrix products on the CPU, on a tiny
+random Qwen3 in fp32; padding rows leave real rows unchanged; a captured graph gives the
+eager result on every replay, with other work between replays; a mixed prefill + decode
+step (``forward_batch``) gives the oracle's logits and the same logits as each sequence
+run alone.
 """
 
 from __future__ import annotations
@@ -17,7 +19,7 @@ import torch.nn.functional as F
 from oracle import ref
 from tinyserve_amd.decode_step import (DecodeGraph, DecodeStep, KVPool, ModelShape, random_context_tables,
                                        random_weights)  # fmt: skip
-from tinyserve_amd.step_inputs import DecodeInputs, PagedTable, fill_decode_inputs
+from tinyserve_amd.step_inputs import Batch, DecodeInputs, PagedTable, build_batch, fill_decode_inputs
 
 pytestmark = pytest.mark.gpu
 DEVICE = "cuda"
@@ -40,12 +42,25 @@ def setup(lens: list[int], rows: int, dtype: torch.dtype = torch.float32, shape:
     return w, pool, tabs, inp
 
 
-def reference_step(shape: ModelShape, w: dict, k: torch.Tensor, v: torch.Tensor, inp: DecodeInputs,
+def reference_step(shape: ModelShape, w: dict, k: torch.Tensor, v: torch.Tensor, inp: DecodeInputs | Batch,
                    block_size: int) -> torch.Tensor:  # fmt: skip
-    """The reference's forward_decode composed from the oracle, fp32 on the CPU; writes k, v."""
+    """The reference's forward_decode (a ``DecodeInputs``) or forward_batch (a ``Batch``:
+    every sequence through the per-sequence prefill reference) composed from the oracle,
+    fp32 on the CPU; logits of every row; writes k, v."""
     cw = {n: t.float().cpu() for n, t in w.items()}
-    tok, pos, slots = inp.token_ids.cpu(), inp.positions.cpu(), inp.slots.cpu()
     bt, lens = inp.block_tables.cpu(), inp.context_lens.cpu()
+    if isinstance(inp, Batch):
+        tok, pos, slots = inp.token_ids.cpu(), inp.positions.cpu(), inp.new_slots.cpu()
+        qs, ql = inp.q_starts.cpu(), inp.q_lens.cpu()
+
+        def attend(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor) -> torch.Tensor:
+            return ref.prefill_ref(q, kc, vc, bt, qs, ql, lens, shape.head_dim**-0.5, block_size)
+    else:
+        tok, pos, slots = inp.token_ids.cpu(), inp.positions.cpu(), inp.slots.cpu()
+
+        def attend(q: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor) -> torch.Tensor:
+            return ref.decode_ref(q, kc, vc, bt, lens, shape.head_dim**-0.5, block_size)
+
     cos, sin = ref.rope_cos_sin(shape.head_dim, shape.rope_theta, pos)
     x = cw["model.embed_tokens.weight"][tok]
     n, s = x.shape[0], shape
@@ -57,7 +72,7 @@ def reference_step(shape: ModelShape, w: dict, k: torch.Tensor, v: torch.Tensor,
             q.reshape(n, s.num_heads, s.head_dim), kk.reshape(n, s.num_kv_heads, s.head_dim),
             vv.reshape(n, s.num_kv_heads, s.head_dim), cw[p + "self_attn.q_norm.weight"],
             cw[p + "self_attn.k_norm.weight"], cos, sin, slots, k[i], v[i], s.rms_norm_eps)  # fmt: skip
-        attn = ref.decode_ref(q, k[i], v[i], bt, lens, s.head_dim**-0.5, block_size)
+        attn = attend(q, k[i], v[i])
         x = x + attn.reshape(n, s.q_size) @ cw[p + "self_attn.o_proj.weight"].T
         h = ref.rms_norm(x, cw[p + "post_attention_layernorm.weight"], s.rms_norm_eps)
         gate, up = (h @ cw[p + "mlp.gate_up_proj.weight"].T).chunk(2, dim=1)
@@ -121,3 +136,60 @@ def test_graph_replays_equal_the_eager_step(dtype: torch.dtype) -> None:
         torch.testing.assert_close(got, want, atol=0, rtol=0)
         assert torch.equal(pool.k, k_after) and torch.equal(pool.v, v_after)
         torch.randn(1 << 20, device=DEVICE).sum().item()  # unrelated eager work between replays
+
+
+def mixed_setup(cached: list[int], new: list[int], seed: int, block_size: int = 4):
+    """A tiny fp32 model, a filled pool and a ``Batch`` of ``new[b]`` tokens per sequence
+    after ``cached[b]`` earlier ones (whose k/v the random pool stands in for)."""
+    w, pool, tabs, _ = setup([c + n for c, n in zip(cached, new)], len(cached), seed=seed, block_size=block_size)
+    g = torch.Generator(device="cpu").manual_seed(seed + 2)
+    items = [(torch.randint(0, TINY.vocab, (n,), generator=g).tolist(), t) for n, t in zip(new, tabs)]
+    return w, pool, tabs, items
+
+
+@pytest.mark.parametrize(
+    "cached,new",
+    [
+        ([5, 0, 9, 2, 0], [3, 7, 1, 1, 1]),  # prefill and decode sequences interleaved
+        ([0, 3], [17, 40]),  # prefill only, one from scratch
+        ([6, 1, 13], [1, 1, 1]),  # decode only
+        ([30], [1]),
+    ],
+)
+def test_mixed_step_matches_the_reference_step(cached: list[int], new: list[int]) -> None:
+    w, pool, tabs, items = mixed_setup(cached, new, seed=11)
+    batch = build_batch(items, DEVICE)
+    kr, vr = pool.k.cpu(), pool.v.cpu()
+    want = reference_step(TINY, w, kr, vr, batch, pool.block_size)[batch.last_rows.cpu()]
+    got = DecodeStep(TINY, w, pool).forward_batch(batch).cpu()
+    assert got.shape == (len(new), TINY.vocab) and got.dtype == torch.float32
+    torch.testing.assert_close(got, want, atol=1e-4, rtol=1e-4)
+    slots = batch.new_slots.cpu()
+    torch.testing.assert_close(pool.k.cpu()[:, slots], kr[:, slots], atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(pool.v.cpu()[:, slots], vr[:, slots], atol=1e-5, rtol=1e-5)
+
+
+def test_mixed_step_equals_each_sequence_alone() -> None:
+    # test_batched_forward.py: a sequence's logits do not depend on what else is batched.
+    cached, new = [4, 0, 11, 7], [1, 9, 1, 5]
+    w, pool, tabs, items = mixed_setup(cached, new, seed=3)
+    k0, v0 = pool.k.clone(), pool.v.clone()
+    step = DecodeStep(TINY, w, pool)
+    together = step.forward_batch(build_batch(items, DEVICE))
+    for b, item in enumerate(items):
+        pool.k.copy_(k0)
+        pool.v.copy_(v0)
+        alone = step.forward_batch(build_batch([item], DEVICE))
+        torch.testing.assert_close(alone[0], together[b], atol=1e-5, rtol=1e-5)
+
+
+def test_decode_only_batch_equals_the_decode_step() -> None:
+    lens = [6, 1, 13, 4]
+    w, pool, tabs, inp = setup(lens, len(lens), seed=5)
+    k0, v0 = pool.k.clone(), pool.v.clone()
+    step = DecodeStep(TINY, w, pool)
+    want = step.forward(inp)
+    pool.k.copy_(k0)
+    pool.v.copy_(v0)
+    got = step.forward_batch(build_batch([([int(t)], tab) for t, tab in zip(inp.token_ids.cpu(), tabs)], DEVICE))
+    torch.testing.assert_close(got, want, atol=0, rtol=0)

@@ -31,8 +31,10 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from tinyserve_amd import hip_attention, hip_fused
-from tinyserve_amd.step_inputs import DecodeInputs
+from collections.abc import Callable
+
+from tinyserve_amd import hip_attention, hip_fused, hip_prefill
+from tinyserve_amd.step_inputs import Batch, DecodeInputs
 
 HEAD_MIN_ROWS = 8  # the output head runs on at least this many rows (model.py:64)
 
@@ -138,8 +140,10 @@ class DecodeStep:
             q, self.pool.k[i], self.pool.v[i], inputs.block_tables, inputs.context_lens,
             self.scale, self.pool.block_size, self.num_splits)  # fmt: skip
 
-    def layer(self, i: int, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-              inputs: DecodeInputs) -> torch.Tensor:  # fmt: skip
+    def layer(self, i: int, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, slots: torch.Tensor,
+              attend: Callable[[int, torch.Tensor], torch.Tensor]) -> torch.Tensor:  # fmt: skip
+        """One decoder layer (model.py:137-179, the fused path): the new tokens' k/v go to
+        the pool at ``slots``; ``attend(i, q)`` returns the attention output for ``q``."""
         s, w, p = self.shape, self.w, f"model.layers.{i}."
         n = x.shape[0]
         h = hip_fused.rms_norm_rows(x, w[p + "input_layernorm.weight"], s.rms_norm_eps)
@@ -148,25 +152,77 @@ class DecodeStep:
         q = hip_fused.qk_norm_rope_store(
             q.view(n, s.num_heads, s.head_dim), k.view(n, s.num_kv_heads, s.head_dim),
             v.view(n, s.num_kv_heads, s.head_dim), w[p + "self_attn.q_norm.weight"],
-            w[p + "self_attn.k_norm.weight"], cos, sin, inputs.slots, self.pool.k[i],
+            w[p + "self_attn.k_norm.weight"], cos, sin, slots, self.pool.k[i],
             self.pool.v[i], s.rms_norm_eps)  # fmt: skip
-        attn = self._attention(i, q, inputs)
+        attn = attend(i, q)
         x = x + F.linear(attn.reshape(n, s.q_size), w[p + "self_attn.o_proj.weight"])
         h = hip_fused.rms_norm_rows(x, w[p + "post_attention_layernorm.weight"], s.rms_norm_eps)
         gate, up = F.linear(h, w[p + "mlp.gate_up_proj.weight"]).chunk(2, dim=1)
         return x + F.linear(F.silu(gate) * up, w[p + "mlp.down_proj.weight"])
 
-    def forward(self, inputs: DecodeInputs) -> torch.Tensor:
+    def _run(self, token_ids: torch.Tensor, positions: torch.Tensor, slots: torch.Tensor,
+             attend: Callable[[int, torch.Tensor], torch.Tensor],
+             rows: torch.Tensor | None = None) -> torch.Tensor:  # fmt: skip
+        """Logits of every token, or of ``rows`` only (model.py:181-211)."""
         s = self.shape
-        cos, sin = rope_tables(s.head_dim, s.rope_theta, inputs.positions)
-        x = self.w["model.embed_tokens.weight"][inputs.token_ids]
+        cos, sin = rope_tables(s.head_dim, s.rope_theta, positions)
+        x = self.w["model.embed_tokens.weight"][token_ids]
         for i in range(s.num_layers):
-            x = self.layer(i, x, cos, sin, inputs)
+            x = self.layer(i, x, cos, sin, slots, attend)
+        if rows is not None:
+            x = x[rows]
         x = hip_fused.rms_norm_rows(x, self.w["model.norm.weight"], s.rms_norm_eps)
         n = x.shape[0]
         if n < HEAD_MIN_ROWS:
             x = F.pad(x, (0, 0, 0, HEAD_MIN_ROWS - n))
         return F.linear(x, self.w["model.embed_tokens.weight"])[:n].float()
+
+    def forward(self, inputs: DecodeInputs) -> torch.Tensor:
+        """One decode step for every row of ``inputs`` (model.py:332-356)."""
+        return self._run(inputs.token_ids, inputs.positions, inputs.slots,
+                         lambda i, q: self._attention(i, q, inputs))  # fmt: skip
+
+    def forward_batch(self, batch: Batch) -> torch.Tensor:
+        """``[B, vocab]`` logits of each sequence's last new token for a mixed step
+        (model.py:255-323 with the kernels): one-token sequences attend through the
+        decode kernel in one launch, the others through the varlen prefill kernel in one
+        launch, both on the rows of one flat batch. Reads the query lengths on the host."""
+        qlens = batch.query_lens
+        starts = [0]
+        for n in qlens[:-1]:
+            starts.append(starts[-1] + n)
+        dev = batch.token_ids.device
+        one = [b for b, n in enumerate(qlens) if n == 1]
+        rest = [b for b, n in enumerate(qlens) if n != 1]
+        scale, bs = self.scale, self.pool.block_size
+
+        def ints(xs: list[int]) -> torch.Tensor:
+            return torch.tensor(xs, dtype=torch.int32, device=dev)
+
+        if one:
+            d_idx = torch.tensor(one, device=dev)
+            d_rows = torch.tensor([starts[b] for b in one], device=dev)
+            d_tables, d_lens = batch.block_tables[d_idx], batch.context_lens[d_idx]
+        if rest:
+            p_idx = torch.tensor(rest, device=dev)
+            p_starts, p_qlens = ints([starts[b] for b in rest]), ints([qlens[b] for b in rest])
+            p_tables, p_lens = batch.block_tables[p_idx], batch.context_lens[p_idx]
+            max_q = max(qlens[b] for b in rest)
+
+        def attend(i: int, q: torch.Tensor) -> torch.Tensor:
+            k, v = self.pool.k[i], self.pool.v[i]
+            if not rest:  # all decode: the rows are the sequences, in order
+                return hip_attention.launch_paged_decode_split(
+                    q, k, v, batch.block_tables, batch.context_lens, scale, bs, self.num_splits)
+            out = torch.empty_like(q)
+            if one:
+                out[d_rows] = hip_attention.launch_paged_decode_split(
+                    q[d_rows], k, v, d_tables, d_lens, scale, bs, self.num_splits)  # fmt: skip
+            hip_prefill.paged_prefill_attention(q, k, v, p_tables, p_starts, p_qlens, p_lens, scale, bs,
+                                                max_q, out)  # fmt: skip
+            return out
+
+        return self._run(batch.token_ids, batch.positions, batch.new_slots, attend, rows=batch.last_rows)
 
     def attention_only(self, inputs: DecodeInputs) -> torch.Tensor:
         """The step's decode-attention launches alone (one per layer, on the current
