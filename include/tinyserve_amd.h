@@ -85,7 +85,9 @@ int ts_decode_combine(const float* m, const float* l, const float* acc, void* ou
  * Sequence r's queries are rows q_starts[r] .. q_starts[r] + q_lens[r] - 1 of q and
  * are its positions context_lens[r] - q_lens[r] .. context_lens[r] - 1; query at
  * position p attends keys 0 .. p of its own block table. Only those rows of `out`
- * are written. max_q_len (>= every q_lens entry) sizes the grid without a host sync.
+ * are written. max_q_len (>= every q_lens entry) sizes the grid without a host sync;
+ * n_rows, the number of rows of q (0 if unknown), only steers the choice of workgroup
+ * shape (mean new tokens per sequence).
  * fp16/bf16 with head_dim 64 or 128 run on MFMA and round the softmax weights to the
  * input dtype before P.V (as the reference kernel does, triton_prefill.py:118); other
  * shapes and fp32 use fp32 FMA throughout.
@@ -93,10 +95,10 @@ int ts_decode_combine(const float* m, const float* l, const float* acc, void* ou
 int ts_prefill_varlen(const void* q, const void* k_cache, const void* v_cache, void* out,
                       const int32_t* block_tables, const int32_t* q_starts,
                       const int32_t* q_lens, const int32_t* context_lens, int R, int Hq,
-                      int Hkv, int D, int block_size, int max_q_len, int64_t q_stride_t,
-                      int64_t q_stride_h, int64_t o_stride_t, int64_t o_stride_h,
-                      int64_t k_stride_slot, int64_t k_stride_head, int64_t bt_stride,
-                      float scale, int dtype, void* stream);
+                      int Hkv, int D, int block_size, int max_q_len, int64_t n_rows,
+                      int64_t q_stride_t, int64_t q_stride_h, int64_t o_stride_t,
+                      int64_t o_stride_h, int64_t k_stride_slot, int64_t k_stride_head,
+                      int64_t bt_stride, float scale, int dtype, void* stream);
 
 /*
  * RMSNorm of every row of x [T, N]:

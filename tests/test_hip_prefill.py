@@ -154,6 +154,8 @@ def test_both_workgroup_shapes(dtype: torch.dtype) -> None:
     # launch has at least two of them per CU, else 4-wave ones (64 queries x 2 heads,
     # 2-stage ring, two per CU). At Qwen3 shapes 4 prompts of up to 2048 tokens make 512
     # 8-wave workgroups (8-wave shape on 256 CUs); 3 make 384 (4-wave shape).
-    for lens in ([2048, 1999, 1100, 700], [2048, 1500, 64]):
+    # 16 prompts of up to 512 tokens (mean under 1280) run the 4-wave, 32-key shape at
+    # three per CU.
+    for lens in ([2048, 1999, 1100, 700], [2048, 1500, 64], [512] * 15 + [77]):
         c = prefill_case([(0, n) for n in lens], 16, 8, 128, 16, dtype, seed=len(lens))
         check(c, run(c))

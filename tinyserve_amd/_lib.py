@@ -39,7 +39,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_prefill_varlen": (
         _i,
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,  # q k v out bt q_starts q_lens ctx_lens
-         _i, _i, _i, _i, _i, _i,  # R Hq Hkv D block_size max_q_len
+         _i, _i, _i, _i, _i, _i, _i64,  # R Hq Hkv D block_size max_q_len n_rows
          _i64, _i64, _i64, _i64, _i64, _i64, _i64,  # strides
          _f, _i, _vp],
     ),

@@ -25,9 +25,12 @@
 // deals workgroups to the 8 XCDs round-robin, with 8 kv heads each head's workgroups
 // share one XCD's L2, where its K/V blocks are re-read by every query tile.
 //
-// Two shapes: 8 waves with a 3-stage ring (one workgroup per CU, 98 KB of LDS) and, for
-// launches with too few query tiles to fill the chip that way, 4 waves with a 2-stage
-// ring (66 KB: two workgroups per CU, half the queries per workgroup).
+// Three shapes: 8 waves with a 3-stage ring of 64-key tiles (one workgroup per CU, 98 KB
+// of LDS, two waves per SIMD); for launches with too few query tiles to fill the chip
+// that way, 4 waves with a 2-stage ring (66 KB: two workgroups per CU, half the queries
+// per workgroup); and for mid-size launches of short prompts, 4 waves over 32-key tiles
+// (a 2-stage ring of 34 KB, 157 VGPRs: three workgroups, so three waves, per SIMD), whose
+// extra wave per SIMD and finer key tiles outweigh the doubled barriers there.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_{f16,bf16}). Scores are computed transposed,
 // S^T[key, query] = K . Q^T, with K as the A operand (one 16-byte LDS read per lane) and
@@ -161,8 +164,8 @@ __device__ __forceinline__ void ring_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <typename T, int D, int HG, int QB, int kWaves, int kStages, int kBN>
-__global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+template <typename T, int D, int HG, int QB, int kWaves, int kStages, int kBN, int kOcc>
+__global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(kOcc, kOcc))) void
 prefill_mfma_kernel(const PrefillArgs a) {
   using V8 = typename Mfma<T>::V8;
   using Sh = TileShape<D, kWaves, kBN>;
@@ -500,11 +503,11 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
 }
 
-template <typename T, int D, int HG, int W, int S, int BN>
+template <typename T, int D, int HG, int W, int S, int BN, int OCC>
 static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream) {
   constexpr int QB = W / HG;
   dim3 grid(static_cast<unsigned>(a.n_qtiles) * a.R * Hkv * a.hchunks);
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN>), grid, dim3(W * kWave), 0, stream, a);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC>), grid, dim3(W * kWave), 0, stream, a);
   return launch_status();
 }
 
@@ -512,7 +515,7 @@ static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream
 // work; the 4-wave shape halves the work per workgroup and fits two workgroups per CU,
 // which wins when the launch has fewer than two 8-wave workgroups per CU (e.g. one
 // 2048-token prompt: 128 workgroups of 8 waves).
-template <typename T, int D, int W, int S, int BN>
+template <typename T, int D, int W, int S, int BN, int OCC>
 static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, hipStream_t stream) {
   const int hg = a.group < W ? a.group : W;
   a.hchunks = a.group / hg;
@@ -520,24 +523,42 @@ static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, hipStream_t str
   a.n_qtiles = (max_q_len + bq - 1) / bq;
   a.n_kvh = Hkv;
   switch (hg) {
-    case 1: return launch_prefill_mfma<T, D, 1, W, S, BN>(a, Hkv, stream);
-    case 2: return launch_prefill_mfma<T, D, 2, W, S, BN>(a, Hkv, stream);
-    case 4: return launch_prefill_mfma<T, D, 4, W, S, BN>(a, Hkv, stream);
+    case 1: return launch_prefill_mfma<T, D, 1, W, S, BN, OCC>(a, Hkv, stream);
+    case 2: return launch_prefill_mfma<T, D, 2, W, S, BN, OCC>(a, Hkv, stream);
+    case 4: return launch_prefill_mfma<T, D, 4, W, S, BN, OCC>(a, Hkv, stream);
     case 8:
-      if constexpr (W >= 8) return launch_prefill_mfma<T, D, 8, W, S, BN>(a, Hkv, stream);
+      if constexpr (W >= 8) return launch_prefill_mfma<T, D, 8, W, S, BN, OCC>(a, Hkv, stream);
       return TS_EUNSUPPORTED;
     default: return TS_EUNSUPPORTED;
   }
 }
 
-template <typename T, int D>
-static int dispatch_hg(PrefillArgs& a, int Hkv, int max_q_len, hipStream_t stream) {
-  const int hg8 = a.group < 8 ? a.group : 8;
+// Which of the three workgroup shapes a launch runs (see the header comment). wg8 is the
+// 8-wave grid. Measured at Qwen3 shapes: small grids (one to two prompts) run the 4-wave,
+// 64-key shape at two per CU; mid-size grids of short prompts (mean new tokens per
+// sequence up to 1280: 8-32 mixed prompts, 16 x 512, 64 x 256) the 4-wave, 32-key shape
+// at three per CU (+5-14%); long prompts and large grids the 8-wave shape.
+enum class PrefillShape { kW8, kW4, kW4Short };
+
+static PrefillShape prefill_shape(int R, int group, int Hkv, int max_q_len, int64_t n_rows) {
+  const int hg8 = group < 8 ? group : 8;
   const int64_t wg8 = static_cast<int64_t>((max_q_len + 32 * (8 / hg8) - 1) / (32 * (8 / hg8))) *
-                      a.R * Hkv * (a.group / hg8);
-  if (a.group <= 4 && wg8 < 2 * static_cast<int64_t>(compute_units()))
-    return dispatch_hg_w<T, D, 4, 2, 64>(a, Hkv, max_q_len, stream);
-  return dispatch_hg_w<T, D, 8, 3, 64>(a, Hkv, max_q_len, stream);
+                      R * Hkv * (group / hg8);
+  const int64_t cus = compute_units();
+  if (group > 4) return PrefillShape::kW8;
+  const bool short_mean = n_rows > 0 && n_rows <= 1280 * static_cast<int64_t>(R);
+  if (short_mean && wg8 >= 2 * cus && wg8 <= 16 * cus) return PrefillShape::kW4Short;
+  if (wg8 < 2 * cus) return PrefillShape::kW4;
+  return PrefillShape::kW8;
+}
+
+template <typename T, int D>
+static int dispatch_hg(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows, hipStream_t stream) {
+  switch (prefill_shape(a.R, a.group, Hkv, max_q_len, n_rows)) {
+    case PrefillShape::kW4Short: return dispatch_hg_w<T, D, 4, 2, 32, 3>(a, Hkv, max_q_len, stream);
+    case PrefillShape::kW4: return dispatch_hg_w<T, D, 4, 2, 64, 2>(a, Hkv, max_q_len, stream);
+    default: return dispatch_hg_w<T, D, 8, 3, 64, 2>(a, Hkv, max_q_len, stream);
+  }
 }
 
 int prefill_rows_generic(const void* q, const void* k, const void* v, void* out,
@@ -555,11 +576,12 @@ extern "C" int ts_prefill_varlen(const void* q, const void* k_cache, const void*
                                  void* out, const int32_t* block_tables,
                                  const int32_t* q_starts, const int32_t* q_lens,
                                  const int32_t* context_lens, int R, int Hq, int Hkv, int D,
-                                 int block_size, int max_q_len, int64_t q_stride_t,
+                                 int block_size, int max_q_len, int64_t n_rows,
+                                 int64_t q_stride_t,
                                  int64_t q_stride_h, int64_t o_stride_t, int64_t o_stride_h,
                                  int64_t k_stride_slot, int64_t k_stride_head,
                                  int64_t bt_stride, float scale, int dtype, void* stream) {
-  if (R < 0 || max_q_len < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || !is_pow2(Hq / Hkv) ||
+  if (R < 0 || max_q_len < 0 || n_rows < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || !is_pow2(Hq / Hkv) ||
       !is_pow2(block_size))
     return TS_EINVAL;
   if (R == 0 || max_q_len == 0) return 0;
@@ -574,11 +596,11 @@ extern "C" int ts_prefill_varlen(const void* q, const void* k_cache, const void*
                   R, Hq / Hkv, 1, lbs, 1, Hkv, q_stride_t, q_stride_h, o_stride_t, o_stride_h,
                   k_stride_slot, k_stride_head, bt_stride, scale * kLog2e};
     if (dtype == TS_F16) {
-      return D == 64 ? dispatch_hg<f16, 64>(a, Hkv, max_q_len, st)
-                     : dispatch_hg<f16, 128>(a, Hkv, max_q_len, st);
+      return D == 64 ? dispatch_hg<f16, 64>(a, Hkv, max_q_len, n_rows, st)
+                     : dispatch_hg<f16, 128>(a, Hkv, max_q_len, n_rows, st);
     }
-    return D == 64 ? dispatch_hg<bf16, 64>(a, Hkv, max_q_len, st)
-                   : dispatch_hg<bf16, 128>(a, Hkv, max_q_len, st);
+    return D == 64 ? dispatch_hg<bf16, 64>(a, Hkv, max_q_len, n_rows, st)
+                   : dispatch_hg<bf16, 128>(a, Hkv, max_q_len, n_rows, st);
   }
   return prefill_rows_generic(q, k_cache, v_cache, out, block_tables, q_starts, q_lens,
                               context_lens, R, Hq, Hkv, D, lbs, max_q_len, q_stride_t,

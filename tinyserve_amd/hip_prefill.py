@@ -97,7 +97,7 @@ def paged_prefill_attention(
         "ts_prefill_varlen",
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
         block_tables.data_ptr(), q_starts.data_ptr(), q_lens.data_ptr(), context_lens.data_ptr(),
-        r, num_q_heads, num_kv_heads, head_dim, block_size, int(max_q_len),
+        r, num_q_heads, num_kv_heads, head_dim, block_size, int(max_q_len), t,
         q.stride(0), q.stride(1), out.stride(0), out.stride(1),
         k_cache.stride(0), k_cache.stride(1), block_tables.stride(0),
         float(scale), _lib.dtype_code(q), _lib.stream_of(dev),
