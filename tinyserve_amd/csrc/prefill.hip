@@ -149,6 +149,24 @@ __device__ __forceinline__ void lds_load16(const void* src, TS_LDS void* dst) {
 #endif
 }
 
+// The same load with a scalar base address and a 32-bit per-lane byte offset
+// (global_load_lds_dwordx4 voffset, saddr): the address arithmetic of a gather whose
+// lanes share one cache block stays on the scalar unit.
+__device__ __forceinline__ void lds_load16_s(const void* base, uint32_t voff, TS_LDS void* dst) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(voff), "s"(base)
+      : "memory");
+#endif
+}
+
 // Wait until at most N of this wave's vector-memory operations are in flight and all its
 // LDS operations are done, then meet the other waves at s_barrier. __syncthreads() would
 // also fence workgroup memory, which waits for every load in flight (vmcnt(0)) and so
@@ -164,7 +182,8 @@ __device__ __forceinline__ void ring_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <typename T, int D, int HG, int QB, int kWaves, int kStages, int kBN, int kOcc>
+template <typename T, int D, int HG, int QB, int kWaves, int kStages, int kBN, int kOcc,
+          bool kScalarIds>
 __global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(kOcc, kOcc))) void
 prefill_mfma_kernel(const PrefillArgs a) {
   using V8 = typename Mfma<T>::V8;
@@ -270,7 +289,44 @@ prefill_mfma_kernel(const PrefillArgs a) {
 
   // Keys past key_end read key_last (finite, owned data): their scores are masked and
   // their V rows meet P = 0.
+  //
+  // kScalarIds (block size >= RPI): the RPI rows of one load lie in one cache block, so
+  // its block id comes from a scalar load of the table (cached in the scalar cache), its
+  // base address is scalar, and a lane adds only its row and 16-byte unit.
+  const TS_CONST int32_t* bt_c = (const TS_CONST int32_t*)(btrow);
+  const uint32_t k_ss_bytes = static_cast<uint32_t>(a.k_ss) * sizeof(T);
+  const uint32_t row_bytes = static_cast<uint32_t>(dma_row) * k_ss_bytes;
+  uint32_t kunit[IPW], vunit[IPW];
+#pragma unroll
+  for (int m = 0; m < IPW; ++m) {
+    const int row = (wave * IPW + m) * RPI + dma_row;
+    kunit[m] = 16u * static_cast<uint32_t>(dma_unit ^ k_swz<D>(row));
+    vunit[m] = 16u * static_cast<uint32_t>(dma_unit ^ v_swz<D>(row));
+  }
   auto gather = [&](T* k_lds, T* v_lds, int n0) {
+    if constexpr (kScalarIds) {
+      // Every id first (scalar loads issued together, one wait), then the loads.
+      int key0[IPW], blk[IPW];
+#pragma unroll
+      for (int m = 0; m < IPW; ++m) {
+        key0[m] = __builtin_amdgcn_readfirstlane(min(n0 + (wave * IPW + m) * RPI, key_last));
+        blk[m] = bt_c[key0[m] >> lbs];
+      }
+#pragma unroll
+      for (int m = 0; m < IPW; ++m) {
+        const int row0 = (wave * IPW + m) * RPI;
+        const uint64_t slot0 = (static_cast<uint64_t>(static_cast<uint32_t>(blk[m])) << lbs) +
+                               static_cast<uint32_t>(key0[m] & bs_mask);
+        const uint64_t boff = slot0 * k_ss_bytes;
+        // Rows past key_last read key_last.
+        const uint32_t voff = min(row_bytes, static_cast<uint32_t>(key_last - key0[m]) * k_ss_bytes);
+        lds_load16_s(reinterpret_cast<const char*>(kbase) + boff, voff + kunit[m],
+                     (TS_LDS void*)(k_lds + row0 * D));
+        lds_load16_s(reinterpret_cast<const char*>(vbase) + boff, voff + vunit[m],
+                     (TS_LDS void*)(v_lds + row0 * D));
+      }
+      return;
+    }
 #pragma unroll
     for (int m = 0; m < IPW; ++m) {
       const int row0 = (wave * IPW + m) * RPI;
@@ -285,6 +341,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
   };
   // Whether the ids of keys up to min(n0 + kBN, key_end) - 1 lie in the window.
   auto in_window = [&](int n0) {
+    if constexpr (kScalarIds) return true;  // no window
     return ((min(n0 + kBN, key_end) - 1) >> lbs) < win_blk0 + kWin;
   };
 
@@ -464,8 +521,10 @@ prefill_mfma_kernel(const PrefillArgs a) {
   T* const k2 = k_ring + (kStages - 1) * TILE;  // == k1 with two stages (never used)
   T* const v2 = v_ring + (kStages - 1) * TILE;
 
-  fill_window(0);
-  __syncthreads();
+  if constexpr (!kScalarIds) {
+    fill_window(0);
+    __syncthreads();
+  }
   gather(k0, v0, 0);
   if constexpr (kStages == 3) {
     if (kBN < key_end) gather(k1, v1, kBN);
@@ -507,7 +566,11 @@ template <typename T, int D, int HG, int W, int S, int BN, int OCC>
 static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream) {
   constexpr int QB = W / HG;
   dim3 grid(static_cast<unsigned>(a.n_qtiles) * a.R * Hkv * a.hchunks);
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC>), grid, dim3(W * kWave), 0, stream, a);
+  // A load's RPI rows share a cache block when blocks hold at least RPI slots.
+  if ((1 << a.lbs) >= TileShape<D, W, BN>::kRPI)
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, true>), grid, dim3(W * kWave), 0, stream, a);
+  else
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, false>), grid, dim3(W * kWave), 0, stream, a);
   return launch_status();
 }
 
