@@ -437,18 +437,22 @@ prefill_mfma_kernel(const PrefillArgs a) {
     // Lazy rescaling without a maximum on the common path: P is first computed against
     // the old running maximum. A lane's sum bounds each of its P, so if no lane's sum
     // exceeds 2^kRescale every P is at most 2^kRescale (exact in fp32, representable in
-    // fp16/bf16) and the tile is done. Otherwise (always on a wave's first tile, whose
-    // m_run is the finite "no maximum" sentinel, and whenever the scores grew by more than
-    // kRescale) the exact maximum is taken, O and l are rescaled, and P is recomputed.
-    float psum = make_p();
-    if (__any(!(psum <= exp2f(kRescale)))) {
+    // fp16/bf16) and the tile is done. Otherwise (whenever the scores grew by more than
+    // kRescale) the exact maximum is taken, O and l are rescaled, and P is recomputed. A
+    // wave's first tile (n0 == 0 for every wave) starts from the exact maximum, so it
+    // needs no second pass: every row has a key there (key 0), so the maximum is finite.
+    auto tile_max = [&]() -> float {
       float mx = s[0][0];
 #pragma unroll
       for (int h = 0; h < NH; ++h)
 #pragma unroll
         for (int v = (h == 0 ? 1 : 0); v < 16; ++v) mx = fmaxf(mx, s[h][v]);
-      mx = halves_max(mx) * c;
-      const float m_new = fmaxf(m_run, mx);
+      return halves_max(mx) * c;
+    };
+    if (n0 == 0) m_run = tile_max();
+    float psum = make_p();
+    if (__any(!(psum <= exp2f(kRescale)))) {
+      const float m_new = fmaxf(m_run, tile_max());
       const float alpha = fast_exp2(m_run - m_new);
       l_run *= alpha;
 #pragma unroll
