@@ -347,6 +347,12 @@ prefill_mfma_kernel(const PrefillArgs a) {
 
   // ---- per-lane constants of the operand reads -------------------------------------------
   const int kphys = k_swz<D>(col);  // K rows col and col + 32 swizzle alike
+  // This lane's K operand of 16-wide chunk kc: row col, 16-byte unit (2 kc + half)
+  // swizzled; the whole offset is kept per chunk, so a read is one address register plus
+  // an immediate (stage and 32-key part).
+  int kofs[KC];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) kofs[kc] = col * D + ((2 * kc + half) ^ kphys) * 8;
   // V^T operand: lane j of its 16-lane group points at V[key0 + j / 4][d0 + 4 (j % 4)].
   const int vj = lane & 15;
   const int vdsub = (lane >> 4) & 1;
@@ -361,11 +367,9 @@ prefill_mfma_kernel(const PrefillArgs a) {
 #pragma unroll
     for (int h = 0; h < NH; ++h) s[h] = f32x16{};
     {
-      const T* kr0 = k_lds + col * D;
       auto kread = [&](int kc, V8 (&x)[NH]) {
-        const int u = ((2 * kc + half) ^ kphys) * 8;
 #pragma unroll
-        for (int h = 0; h < NH; ++h) x[h] = *reinterpret_cast<const V8*>(kr0 + 32 * h * D + u);
+        for (int h = 0; h < NH; ++h) x[h] = *reinterpret_cast<const V8*>(k_lds + kofs[kc] + 32 * h * D);
       };
       V8 ka[2][NH];
       kread(0, ka[0]);
