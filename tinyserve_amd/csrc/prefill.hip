@@ -15,9 +15,13 @@
 // (global_load_lds_dwordx4: lane l's 16 bytes land at the instruction's LDS base +
 // 16 l), through a ring of three stages: while tile t is computed, tiles t + 1 and t + 2
 // are in flight. No registers stage the data and no LDS store instructions are issued.
-// Block ids are staged in LDS (a window of 512 table entries, refilled when a gather
-// passes its end), so the vector-memory counter covers exactly the ring's loads and each
-// stage is waited for with an exact vmcnt.
+// One load instruction covers RPI consecutive keys (4 at D=128). When a cache block holds
+// at least RPI slots those keys share one block, so the block id is a scalar load of the
+// table and the address a scalar base plus a per-lane row/unit offset: the gather costs
+// the VALU almost nothing. Smaller blocks take per-lane ids from a window of 512 table
+// entries staged in LDS (refilled when a gather passes its end). Either way the
+// vector-memory counter covers exactly the ring's loads and each stage is waited for with
+// an exact vmcnt.
 //
 // Dispatch order. Workgroup b = (tile_rev * R + r) * heads + head: every sequence's last
 // query tile (the one with the most keys) is dispatched, for all kv heads, before any
