@@ -156,18 +156,12 @@ __device__ __forceinline__ void lds_load16(const void* src, TS_LDS void* dst) {
 // The same load with a scalar base address and a 32-bit per-lane byte offset
 // (global_load_lds_dwordx4 voffset, saddr): the address arithmetic of a gather whose
 // lanes share one cache block stays on the scalar unit.
+// M0 is bound through the asm operand, so the compiler sets it (one instruction) and
+// knows it is taken.
 __device__ __forceinline__ void lds_load16_s(const void* base, uint32_t voff, TS_LDS void* dst) {
 #if defined(__HIP_DEVICE_COMPILE__)
   const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dwordx4 %2, %3\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds), "v"(voff), "s"(base)
-      : "memory");
+  asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(base), "{m0}"(lds) : "memory");
 #endif
 }
 
@@ -300,15 +294,37 @@ prefill_mfma_kernel(const PrefillArgs a) {
   const TS_CONST int32_t* bt_c = (const TS_CONST int32_t*)(btrow);
   const uint32_t k_ss_bytes = static_cast<uint32_t>(a.k_ss) * sizeof(T);
   const uint32_t row_bytes = static_cast<uint32_t>(dma_row) * k_ss_bytes;
-  uint32_t kunit[IPW], vunit[IPW];
+  uint32_t kunit[IPW], vunit[IPW], rows_bytes[IPW];
 #pragma unroll
   for (int m = 0; m < IPW; ++m) {
     const int row = (wave * IPW + m) * RPI + dma_row;
     kunit[m] = 16u * static_cast<uint32_t>(dma_unit ^ k_swz<D>(row));
     vunit[m] = 16u * static_cast<uint32_t>(dma_unit ^ v_swz<D>(row));
+    rows_bytes[m] = static_cast<uint32_t>(m * RPI + dma_row) * k_ss_bytes;
   }
+  // A wave's IPW * RPI rows of a tile share one block when blocks hold that many slots.
+  const bool wave_block = (1 << lbs) >= IPW * RPI;
   auto gather = [&](T* k_lds, T* v_lds, int n0) {
     if constexpr (kScalarIds) {
+      if (wave_block) {
+        // One block id and one base for all of the wave's loads; rows past key_last
+        // read key_last, which lies in the same block.
+        const int kw = __builtin_amdgcn_readfirstlane(min(n0 + wave * IPW * RPI, key_last));
+        const int blk = bt_c[kw >> lbs];
+        const uint64_t boff = ((static_cast<uint64_t>(static_cast<uint32_t>(blk)) << lbs) +
+                               static_cast<uint32_t>(kw & bs_mask)) * k_ss_bytes;
+        const uint32_t lim = static_cast<uint32_t>(key_last - kw) * k_ss_bytes;
+        const char* kb = reinterpret_cast<const char*>(kbase) + boff;
+        const char* vb = reinterpret_cast<const char*>(vbase) + boff;
+#pragma unroll
+        for (int m = 0; m < IPW; ++m) {
+          const int row0 = (wave * IPW + m) * RPI;
+          const uint32_t voff = min(rows_bytes[m], lim);
+          lds_load16_s(kb, voff + kunit[m], (TS_LDS void*)(k_lds + row0 * D));
+          lds_load16_s(vb, voff + vunit[m], (TS_LDS void*)(v_lds + row0 * D));
+        }
+        return;
+      }
       // Every id first (scalar loads issued together, one wait), then the loads.
       int key0[IPW], blk[IPW];
 #pragma unroll
