@@ -118,12 +118,15 @@ def test_random_batches(specs: list[tuple[int, int]], shape: tuple[int, int, int
     check(c, run(c, rows_per_tile=16, block_n=16))
 
 
-@settings(max_examples=25, deadline=None)
+@settings(max_examples=60, deadline=None)
 @given(
     specs=st.lists(st.tuples(st.integers(0, 150), st.integers(1, 150)), min_size=1, max_size=4),
     heads=st.sampled_from([(8, 8), (8, 4), (8, 2), (8, 1)]),
     head_dim=st.sampled_from([64, 128]),
-    block_size=st.sampled_from([1, 4, 16]),
+    # The gather has three paths by block size: ids staged in LDS (a load's rows span
+    # blocks: 1, 2, and 4 at head_dim 64), a scalar id per load, and one scalar id per
+    # wave and tile (8 and up at the 32-key shape, 16 and up at the 4-wave 64-key shape).
+    block_size=st.sampled_from([1, 2, 4, 8, 16, 32]),
     dtype=st.sampled_from([torch.float16, torch.bfloat16]),
     seed=st.integers(0, 2**16),
 )
@@ -158,4 +161,15 @@ def test_both_workgroup_shapes(dtype: torch.dtype) -> None:
     # three per CU.
     for lens in ([2048, 1999, 1100, 700], [2048, 1500, 64], [512] * 15 + [77]):
         c = prefill_case([(0, n) for n in lens], 16, 8, 128, 16, dtype, seed=len(lens))
+        check(c, run(c))
+
+
+@pytest.mark.parametrize("block_size", [1, 2, 4, 8, 16, 32, 64])
+@pytest.mark.parametrize("shape", [(16, 8, 128), (8, 2, 64)])
+def test_every_gather_path_on_every_workgroup_shape(block_size: int, shape: tuple[int, int, int]) -> None:
+    # Each launch below runs one of the three workgroup shapes (one prompt: 4 waves,
+    # 64-key tiles; 16 prompts of 512: 4 waves, 32-key tiles; 4 x 2048: 8 waves), with
+    # prefix hits so that tiles start mid-block, at every block size.
+    for specs in ([(70, 300)], [(33, 512)] * 15 + [(5, 77)], [(100, 2048)] * 4):
+        c = prefill_case(specs, *shape, block_size, torch.float16, seed=block_size)
         check(c, run(c))
