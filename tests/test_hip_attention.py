@@ -235,6 +235,28 @@ def test_every_workgroup_width_gives_the_reference(batch: int, splits: int) -> N
     assert_matches(out, want, torch.float16, f"B={batch} splits={splits}")
 
 
+@pytest.mark.parametrize("batch", [33, 45, 64])
+@pytest.mark.parametrize("kind", ["mixed", "equal", "one_long"])
+def test_sequences_paired_by_length(batch: int, kind: str) -> None:
+    # At Qwen3 shapes 33-64 sequences run paired by length: workgroup y takes the
+    # sequences ranked y and B - 1 - y (longest first, ties by index) and shares its four
+    # waves between them by length; an odd batch leaves the middle one alone. Lengths
+    # 1 .. 1000 in a scrambled order, all equal (ties only), and one long among short.
+    if kind == "mixed":
+        lens = [1 + (389 * i) % 1000 for i in range(batch)]
+    elif kind == "equal":
+        lens = [300] * batch
+    else:
+        lens = [7] * batch
+        lens[batch // 3] = 1500
+    c = decode_case(lens, dtype=torch.float16, seed=batch)
+    want = oracle32(c)
+    g = on_gpu(c)
+    out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, num_splits=1)
+    assert torch.isfinite(out).all()
+    assert_matches(out, want, torch.float16, f"B={batch} {kind}")
+
+
 @pytest.mark.parametrize("splits", [2, 3, 4])
 def test_partials_and_combine_at_small_split_counts(splits: int) -> None:
     # launch_paged_decode_split runs up to 4 splits inside one workgroup; the C entry's

@@ -72,6 +72,8 @@ struct AttendArgs {
   int splits;
   int wpg;        // waves per workgroup (decode), 1 for prefill
   int max_q_len;  // prefill only
+  int by_length;  // decode: workgroup y takes the sequences of length rank y and nseq-1-y
+  int nseq;       // decode: sequences in the batch
   int64_t q_sb, q_sh, o_sb, o_sh, k_ss, k_sh, bt_s;
   float scale_log2;  // softmax scale * log2(e)
 };
@@ -198,6 +200,37 @@ __device__ __forceinline__ void merge_group_waves(const Args& a, const State& st
 // states merge to an empty state without inf - inf.
 constexpr float kNoMax = -1.0e30f;
 
+// A workgroup of a length pair (one split): each wave parks up to two merged states, one
+// per sequence it walked (slot tag 0: the pair's first sequence, 1: its second, -1:
+// none), then thread t of the group produces element t of each sequence's output over
+// the slots tagged for it.
+template <typename T, int D, int HT>
+struct PairSlots {
+  float m[kMaxWavesPerGroup][2][HT], l[kMaxWavesPerGroup][2][HT];
+  float acc[kMaxWavesPerGroup][2][HT][D];
+  int tag[kMaxWavesPerGroup][2];
+};
+
+template <typename T, int D, int HT, typename State>
+__device__ __forceinline__ void park_state(PairSlots<T, D, HT>& ps, const State& st, int wave,
+                                           int slot, int tag, int c) {
+  using S = RowShape<T, D>;
+  constexpr int NV = S::kNV, VEC = S::kVec, LPT = S::kLPT;
+  if (c < 0) return;
+  if (c == 0) ps.tag[wave][slot] = tag;
+#pragma unroll
+  for (int g = 0; g < HT; ++g) {
+    if (c == 0) {
+      ps.m[wave][slot][g] = st.m[g];
+      ps.l[wave][slot][g] = st.l[g];
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) ps.acc[wave][slot][g][(i * LPT + c) * VEC + j] = st.acc[g][i * VEC + j];
+  }
+}
+
 template <typename T, int D, int HT, bool PREFILL>
 __global__ __launch_bounds__(PREFILL ? kWave : kWave * kMaxWavesPerGroup)
 __attribute__((amdgpu_waves_per_eu(TS_DECODE_WAVES_PER_EU)))
@@ -217,6 +250,9 @@ void paged_attend_kernel(const AttendArgs a) {
 
   int seq, ctx, split = 0;
   int64_t qrow, orow;
+  // Length pairs: the two sequences, and this wave's segments (sequence, block range).
+  int pair_a = -1, pair_b = -1, nseg = 1;
+  int seg_seq[2] = {0, 0}, seg_first[2] = {0, 0}, seg_last[2] = {0, 0};
   if constexpr (PREFILL) {
     seq = blockIdx.x / a.max_q_len;
     const int i = blockIdx.x - seq * a.max_q_len;
@@ -228,6 +264,39 @@ void paged_attend_kernel(const AttendArgs a) {
     orow = row * a.o_sb;
   } else {
     seq = blockIdx.y;
+    if (a.by_length) {
+      // Workgroup y takes the sequences ranked y and B - 1 - y by length (longest
+      // first, ties by index): lane b ranks sequence b against the others (B <= 64).
+      // Its waves are shared between the two in proportion to their lengths, so every
+      // workgroup has about the same work and all run in one round.
+      const int B = a.nseq;
+      const int mine = lane < B ? a.lens[lane] : -1;
+      int rank = 0;
+      for (int j = 0; j < B; ++j) {
+        const int other = __builtin_amdgcn_readlane(mine, j);
+        rank += (other > mine) | ((other == mine) & (j < lane));
+      }
+      const int ra = blockIdx.y, rb = B - 1 - ra;
+      pair_a = __builtin_ctzll(__ballot(lane < B && rank == ra));
+      pair_b = rb != ra ? __builtin_ctzll(__ballot(lane < B && rank == rb)) : -1;
+      // The waves take equal shares of the two sequences' blocks laid end to end; at
+      // most one wave's share straddles both, and it walks them one after the other.
+      const int bmask = (1 << a.lbs) - 1;
+      const int n_a = (a.lens[pair_a] + bmask) >> a.lbs;
+      const int n_b = pair_b >= 0 ? (a.lens[pair_b] + bmask) >> a.lbs : 0;
+      const int share = (n_a + n_b + a.wpg - 1) / a.wpg;
+      const int lo = min(wave * share, n_a + n_b), hi = min(lo + share, n_a + n_b);
+      nseg = 0;
+      if (lo < n_a) {
+        seg_seq[nseg] = pair_a, seg_first[nseg] = lo, seg_last[nseg] = min(hi, n_a);
+        ++nseg;
+      }
+      if (hi > n_a) {
+        seg_seq[nseg] = pair_b, seg_first[nseg] = max(lo, n_a) - n_a, seg_last[nseg] = hi - n_a;
+        ++nseg;
+      }
+      seq = pair_a;
+    }
     split = blockIdx.z;
     ctx = a.lens[seq];
     qrow = seq * a.q_sb;
@@ -236,11 +305,25 @@ void paged_attend_kernel(const AttendArgs a) {
   const int lbs = a.lbs;
   const int bs_mask = (1 << lbs) - 1;
   const int nblocks = (ctx + bs_mask) >> lbs;
-  const int ranges = a.splits * a.wpg;
+  const int ranges = a.splits * (PREFILL ? 1 : a.wpg);
   const int per = (nblocks + ranges - 1) / ranges;
-  const int first = (split * a.wpg + wave) * per;
-  const int last = min(first + per, nblocks);
+  int first = (split * (PREFILL ? 1 : a.wpg) + wave) * per;
+  int last = min(first + per, nblocks);
+  bool pair = false;
+  if constexpr (!PREFILL) pair = a.by_length;
+  if (!pair) seg_seq[0] = seq, seg_first[0] = first, seg_last[0] = last;
 
+  TokenState<T, D, HT> st;
+  __shared__ PairSlots<T, D, HT> pslots;
+  if (pair && lane < 2) pslots.tag[wave][lane] = -1;
+  for (int sgi = 0; sgi < nseg; ++sgi) {
+  if (pair) {
+    seq = seg_seq[sgi];
+    ctx = a.lens[seq];
+    qrow = seq * a.q_sb;
+    first = seg_first[sgi];
+    last = seg_last[sgi];
+  }
   const T* qp = static_cast<const T*>(a.q) + qrow;
   Pack16<T> qv[HT][NV];
 #pragma unroll
@@ -248,7 +331,6 @@ void paged_attend_kernel(const AttendArgs a) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) qv[g][i] = load16(qp + (h0 + g) * a.q_sh + (i * LPT + c) * VEC);
 
-  TokenState<T, D, HT> st;
 #pragma unroll
   for (int g = 0; g < HT; ++g) {
     st.m[g] = kNoMax;
@@ -345,7 +427,33 @@ void paged_attend_kernel(const AttendArgs a) {
   }
 
   merge_token_lanes(st);
+  if (pair) park_state(pslots, st, wave, sgi, seq == pair_a ? 0 : 1, tl == 0 ? c : -1);
+  }  // segments
   if constexpr (!PREFILL) {
+    if (pair) {
+      __syncthreads();
+      const int W = a.wpg;
+      const int parts = pair_b >= 0 ? 2 : 1;
+      for (int t = threadIdx.x; t < parts * HT * D; t += W * kWave) {
+        const int pi = t / (HT * D);
+        const int g = (t % (HT * D)) / D, d = t % D;
+        float mm = kNoMax;
+        for (int w = 0; w < W; ++w)
+          for (int sl = 0; sl < 2; ++sl)
+            if (pslots.tag[w][sl] == pi) mm = fmaxf(mm, pslots.m[w][sl][g]);
+        float den = 0.f, num = 0.f;
+        for (int w = 0; w < W; ++w)
+          for (int sl = 0; sl < 2; ++sl)
+            if (pslots.tag[w][sl] == pi) {
+              const float f = fast_exp2(pslots.m[w][sl][g] - mm);
+              den = fmaf(f, pslots.l[w][sl][g], den);
+              num = fmaf(f, pslots.acc[w][sl][g][d], num);
+            }
+        const int64_t row = static_cast<int64_t>(pi ? pair_b : pair_a) * a.o_sb;
+        static_cast<T*>(a.out)[row + (h0 + g) * a.o_sh + d] = from_f32<T>(num / den);
+      }
+      return;
+    }
     if (a.wpg > 1) {
       merge_group_waves<T, D, HT>(a, st, wave, tl == 0 ? c : -1, seq, h0, split, orow);
       return;
@@ -466,7 +574,7 @@ int prefill_rows_generic(const void* q, const void* k, const void* v, void* out,
   const int ht = head_tile_for(group, 0);
   if (ht < 0) return TS_EINVAL;
   AttendArgs a{q, k, v, bt, ctx_lens, out, nullptr, nullptr, nullptr, q_starts, q_lens,
-               Hq, group, lbs, 1, 1, max_q_len, q_st, q_sh, o_st, o_sh, k_ss, k_sh, bt_s,
+               Hq, group, lbs, 1, 1, max_q_len, 0, 0, q_st, q_sh, o_st, o_sh, k_ss, k_sh, bt_s,
                scale * kLog2e};
   dim3 grid(static_cast<unsigned>(R) * max_q_len, Hq / ht, 1);
   return dispatch_attend<true>(a, dtype, D, ht, grid, stream);
@@ -497,11 +605,20 @@ extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v
   const int64_t want = 4 * static_cast<int64_t>(compute_units());
   int wpg = 1;
   while (wpg < kMaxWavesPerGroup && waves * wpg * 2 <= want) wpg *= 2;
+  // Up to 64 sequences whose workgroups are two-wave (one round of them fills the chip):
+  // pair sequences by length instead, the longest with the shortest, in four-wave
+  // workgroups. A batch of equal contexts runs exactly as before (two waves per
+  // sequence); one of mixed lengths no longer waits on its longest sequences.
+  int by_length = B <= kWave && B >= 2 && splits == 1 && wpg == 2 ? 1 : 0;
+#ifdef DEC_ENV
+  if (getenv("TS_BYLEN")) by_length = by_length && atoi(getenv("TS_BYLEN"));
+#endif
+  if (by_length) wpg = kMaxWavesPerGroup;
   AttendArgs a{q, k_cache, v_cache, block_tables, context_lens, out, m, l, acc, nullptr,
-               nullptr, Hq, group, ilog2(block_size), splits, wpg, 0, q_stride_b, q_stride_h,
-               o_stride_b, o_stride_h, k_stride_slot, k_stride_head, bt_stride,
+               nullptr, Hq, group, ilog2(block_size), splits, wpg, 0, by_length, B, q_stride_b,
+               q_stride_h, o_stride_b, o_stride_h, k_stride_slot, k_stride_head, bt_stride,
                scale * kLog2e};
-  dim3 grid(Hq / ht, B, splits);
+  dim3 grid(Hq / ht, by_length ? (B + 1) / 2 : B, splits);
   return dispatch_attend<false>(a, dtype, D, ht, grid, static_cast<hipStream_t>(stream));
 }
 
