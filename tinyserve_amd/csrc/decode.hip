@@ -20,6 +20,14 @@
 // so that the grid holds about four waves per CU (the kernel needs more than 256 VGPRs,
 // so a SIMD runs one wave of it, and a CU wants four in flight to cover HBM latency).
 //
+// Length pairs. A batch of at most 64 sequences that would get two-wave workgroups is
+// run as pairs instead: workgroup y takes the sequences ranked y and B - 1 - y by
+// length (longest with shortest), and its four waves take equal shares of the two
+// sequences' blocks laid end to end (one wave may walk the end of one and the start of
+// the other). Every workgroup then has about the same work, so a batch of mixed
+// lengths does not wait on its longest sequences; equal lengths give the two-wave
+// layout again.
+//
 // Softmax. Every token lane keeps its own running (max, sum, acc) per query head (the
 // online softmax of triton_attention.py:14-22, in base 2), so the loop has no
 // cross-lane work except the LPT-lane dot-product reduction. The token lanes are
