@@ -54,6 +54,7 @@
 // LDS layout: K and V tiles are [64 keys][D], rows unpadded, their 16-byte units
 // XOR-swizzled per row (K by row & 15, V by a 4-row pattern), which keeps the K operand
 // reads and the transposing V reads free of bank conflicts.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -101,6 +102,7 @@ struct PrefillArgs {
   int lbs;
   int n_qtiles;
   int n_kvh;
+  int seq_group;  // > 0: dispatch in groups of this many sequences ranked by length
   int64_t q_st, q_sh, o_st, o_sh, k_ss, k_sh, bt_s;
   float scale_log2;
 };
@@ -215,8 +217,31 @@ prefill_mfma_kernel(const PrefillArgs a) {
   const int bid = blockIdx.x;
   const int rest = bid / n_hc;
   const int hcx = bid - rest * n_hc;
-  const int tile_rev = rest / a.R;
-  const int r = rest - tile_rev * a.R;
+  int tile_rev, r;
+  if (a.seq_group > 0) {
+    // Groups of seq_group sequences of similar length, longest group first; within a
+    // group, heaviest query tiles first. A group's K/V (one kv head per XCD) stays in
+    // that XCD's L2 while its tiles run, which the plain order below loses when many
+    // sequences are in flight at once. Lane b ranks sequence b by context length
+    // (ties by index; R <= 64).
+    const int per_group = a.n_qtiles * a.seq_group;
+    const int gi = rest / per_group;
+    const int rem = rest - gi * per_group;
+    tile_rev = rem / a.seq_group;
+    const int want = gi * a.seq_group + (rem - tile_rev * a.seq_group);
+    if (want >= a.R) return;
+    const int ln = threadIdx.x & (kWave - 1);
+    const int mine = ln < a.R ? a.ctx_lens[ln] : -1;
+    int rank = 0;
+    for (int j = 0; j < a.R; ++j) {
+      const int other = __builtin_amdgcn_readlane(mine, j);
+      rank += (other > mine) | ((other == mine) & (j < ln));
+    }
+    r = __builtin_ctzll(__ballot(ln < a.R && rank == want));
+  } else {
+    tile_rev = rest / a.R;
+    r = rest - tile_rev * a.R;
+  }
   const int q_len = a.q_lens[r];
   const int tile = (q_len + BQ - 1) / BQ - 1 - tile_rev;
   if (tile < 0) return;
@@ -593,7 +618,8 @@ prefill_mfma_kernel(const PrefillArgs a) {
 template <typename T, int D, int HG, int W, int S, int BN, int OCC>
 static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream) {
   constexpr int QB = W / HG;
-  dim3 grid(static_cast<unsigned>(a.n_qtiles) * a.R * Hkv * a.hchunks);
+  const int seqs = a.seq_group > 0 ? (a.R + a.seq_group - 1) / a.seq_group * a.seq_group : a.R;
+  dim3 grid(static_cast<unsigned>(a.n_qtiles) * seqs * Hkv * a.hchunks);
   // A load's RPI rows share a cache block when blocks hold at least RPI slots.
   if ((1 << a.lbs) >= TileShape<D, W, BN>::kRPI)
     hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, true>), grid, dim3(W * kWave), 0, stream, a);
@@ -607,12 +633,25 @@ static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream
 // which wins when the launch has fewer than two 8-wave workgroups per CU (e.g. one
 // 2048-token prompt: 128 workgroups of 8 waves).
 template <typename T, int D, int W, int S, int BN, int OCC>
-static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, hipStream_t stream) {
+static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows, hipStream_t stream) {
   const int hg = a.group < W ? a.group : W;
   a.hchunks = a.group / hg;
   const int bq = 32 * (W / hg);
   a.n_qtiles = (max_q_len + bq - 1) / bq;
   a.n_kvh = Hkv;
+  // Length-ranked groups of 4096 / (mean new tokens) sequences (1 to 8, at most R: a
+  // group's K/V about fits one XCD's L2), for 8-16 sequences or short prompts (mean up
+  // to 512 new tokens), up to 64 sequences. Measured at Qwen3 shapes: +43% on 8 mixed
+  // prompts, +27% on 64 x 256, +5% on 16 x 512; on 32 mixed prompts (-3%) and a few long
+  // ones (-2.6% at 4 x 2048) the plain order is kept.
+  a.seq_group = 0;
+  if (a.R > 1 && a.R <= kWave && n_rows > 0) {
+    const int64_t mean = (n_rows + a.R - 1) / a.R;
+    if ((a.R >= 8 && a.R <= 16) || mean <= 512) {
+      const int g = static_cast<int>(std::min<int64_t>(8, std::max<int64_t>(1, 4096 / std::max<int64_t>(mean, 1))));
+      a.seq_group = g < a.R ? g : a.R;
+    }
+  }
   switch (hg) {
     case 1: return launch_prefill_mfma<T, D, 1, W, S, BN, OCC>(a, Hkv, stream);
     case 2: return launch_prefill_mfma<T, D, 2, W, S, BN, OCC>(a, Hkv, stream);
@@ -646,9 +685,9 @@ static PrefillShape prefill_shape(int R, int group, int Hkv, int max_q_len, int6
 template <typename T, int D>
 static int dispatch_hg(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows, hipStream_t stream) {
   switch (prefill_shape(a.R, a.group, Hkv, max_q_len, n_rows)) {
-    case PrefillShape::kW4Short: return dispatch_hg_w<T, D, 4, 2, 32, 3>(a, Hkv, max_q_len, stream);
-    case PrefillShape::kW4: return dispatch_hg_w<T, D, 4, 2, 64, 2>(a, Hkv, max_q_len, stream);
-    default: return dispatch_hg_w<T, D, 8, 3, 64, 2>(a, Hkv, max_q_len, stream);
+    case PrefillShape::kW4Short: return dispatch_hg_w<T, D, 4, 2, 32, 3>(a, Hkv, max_q_len, n_rows, stream);
+    case PrefillShape::kW4: return dispatch_hg_w<T, D, 4, 2, 64, 2>(a, Hkv, max_q_len, n_rows, stream);
+    default: return dispatch_hg_w<T, D, 8, 3, 64, 2>(a, Hkv, max_q_len, n_rows, stream);
   }
 }
 
@@ -684,7 +723,7 @@ extern "C" int ts_prefill_varlen(const void* q, const void* k_cache, const void*
                        (reinterpret_cast<uintptr_t>(v_cache) % 16 == 0);
   if ((dtype == TS_F16 || dtype == TS_BF16) && (D == 64 || D == 128) && aligned) {
     PrefillArgs a{q, k_cache, v_cache, out, block_tables, q_starts, q_lens, context_lens,
-                  R, Hq / Hkv, 1, lbs, 1, Hkv, q_stride_t, q_stride_h, o_stride_t, o_stride_h,
+                  R, Hq / Hkv, 1, lbs, 1, Hkv, 0, q_stride_t, q_stride_h, o_stride_t, o_stride_h,
                   k_stride_slot, k_stride_head, bt_stride, scale * kLog2e};
     if (dtype == TS_F16) {
       return D == 64 ? dispatch_hg<f16, 64>(a, Hkv, max_q_len, n_rows, st)
