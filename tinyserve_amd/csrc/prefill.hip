@@ -664,10 +664,11 @@ static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows,
 }
 
 // Which of the three workgroup shapes a launch runs (see the header comment). wg8 is the
-// 8-wave grid. Measured at Qwen3 shapes: small grids (one to two prompts) run the 4-wave,
-// 64-key shape at two per CU; mid-size grids of short prompts (mean new tokens per
-// sequence up to 1280: 8-32 mixed prompts, 16 x 512, 64 x 256) the 4-wave, 32-key shape
-// at three per CU (+5-14%); long prompts and large grids the 8-wave shape.
+// 8-wave grid. Measured at Qwen3 shapes: chunks of at most 128 new tokens (prefix hits)
+// run the 8-wave shape (+2.5-9.5%); small grids (one to two prompts) the 4-wave, 64-key
+// shape at two per CU; mid-size grids of short prompts (mean new tokens per sequence up
+// to 1280: 8-32 mixed prompts, 16 x 512, 64 x 256) the 4-wave, 32-key shape at three per
+// CU (+5-14%); long prompts and large grids the 8-wave shape.
 enum class PrefillShape { kW8, kW4, kW4Short };
 
 static PrefillShape prefill_shape(int R, int group, int Hkv, int max_q_len, int64_t n_rows) {
@@ -676,6 +677,9 @@ static PrefillShape prefill_shape(int R, int group, int Hkv, int max_q_len, int6
                       R * Hkv * (group / hg8);
   const int64_t cus = compute_units();
   if (group > 4) return PrefillShape::kW8;
+  // Up to 128 new tokens per sequence: one 8-wave query tile holds a whole sequence, so
+  // its K/V (the whole cached prefix) is read once per kv head, not once per 64 queries.
+  if (max_q_len <= 128) return PrefillShape::kW8;
   const bool short_mean = n_rows > 0 && n_rows <= 1280 * static_cast<int64_t>(R);
   if (short_mean && wg8 >= 2 * cus && wg8 <= 16 * cus) return PrefillShape::kW4Short;
   if (wg8 < 2 * cus) return PrefillShape::kW4;
