@@ -236,16 +236,25 @@ def test_every_workgroup_width_gives_the_reference(batch: int, splits: int) -> N
 
 
 @pytest.mark.parametrize("batch", [33, 45, 64])
-@pytest.mark.parametrize("kind", ["mixed", "equal", "one_long"])
+@pytest.mark.parametrize("kind", ["mixed", "equal", "one_long", "descending", "ties", "ones"])
 def test_sequences_paired_by_length(batch: int, kind: str) -> None:
     # At Qwen3 shapes 33-64 sequences run paired by length: workgroup y takes the
     # sequences ranked y and B - 1 - y (longest first, ties by index) and shares its four
     # waves between them by length; an odd batch leaves the middle one alone. Lengths
-    # 1 .. 1000 in a scrambled order, all equal (ties only), and one long among short.
+    # 1 .. 1000 in a scrambled order, all equal (ties only), one long among short, already
+    # in rank order (ranking skipped) with ties, five lengths scrambled, and one token each
+    # (waves left with nothing to walk).
     if kind == "mixed":
         lens = [1 + (389 * i) % 1000 for i in range(batch)]
     elif kind == "equal":
         lens = [300] * batch
+    elif kind == "descending":
+        lens = sorted((1 + (389 * i) % 1000 for i in range(batch)), reverse=True)
+        lens[5] = lens[6] = lens[7]
+    elif kind == "ties":
+        lens = [1 + (7 * i % 5) * 200 for i in range(batch)]
+    elif kind == "ones":
+        lens = [1] * batch
     else:
         lens = [7] * batch
         lens[batch // 3] = 1500

@@ -209,23 +209,20 @@ __device__ __forceinline__ void merge_group_waves(const Args& a, const State& st
 constexpr float kNoMax = -1.0e30f;
 
 // A workgroup of a length pair (one split): each wave parks up to two merged states, one
-// per sequence it walked (slot tag 0: the pair's first sequence, 1: its second, -1:
-// none), then thread t of the group produces element t of each sequence's output over
-// the slots tagged for it.
+// per sequence it walked, in walking order (slot 0, then slot 1), then thread t of the
+// group produces element t of each sequence's output over the waves that walked it.
 template <typename T, int D, int HT>
 struct PairSlots {
   float m[kMaxWavesPerGroup][2][HT], l[kMaxWavesPerGroup][2][HT];
   float acc[kMaxWavesPerGroup][2][HT][D];
-  int tag[kMaxWavesPerGroup][2];
 };
 
 template <typename T, int D, int HT, typename State>
 __device__ __forceinline__ void park_state(PairSlots<T, D, HT>& ps, const State& st, int wave,
-                                           int slot, int tag, int c) {
+                                           int slot, int c) {
   using S = RowShape<T, D>;
   constexpr int NV = S::kNV, VEC = S::kVec, LPT = S::kLPT;
   if (c < 0) return;
-  if (c == 0) ps.tag[wave][slot] = tag;
 #pragma unroll
   for (int g = 0; g < HT; ++g) {
     if (c == 0) {
@@ -259,7 +256,7 @@ void paged_attend_kernel(const AttendArgs a) {
   int seq, ctx, split = 0;
   int64_t qrow, orow;
   // Length pairs: the two sequences, and this wave's segments (sequence, block range).
-  int pair_a = -1, pair_b = -1, nseg = 1;
+  int pair_a = -1, pair_b = -1, len_a = 0, len_b = 0, n_a = 0, share = 1, nseg = 1;
   int seg_seq[2] = {0, 0}, seg_first[2] = {0, 0}, seg_last[2] = {0, 0};
   if constexpr (PREFILL) {
     seq = blockIdx.x / a.max_q_len;
@@ -279,20 +276,27 @@ void paged_attend_kernel(const AttendArgs a) {
       // workgroup has about the same work and all run in one round.
       const int B = a.nseq;
       const int mine = lane < B ? a.lens[lane] : -1;
-      int rank = 0;
-      for (int j = 0; j < B; ++j) {
-        const int other = __builtin_amdgcn_readlane(mine, j);
-        rank += (other > mine) | ((other == mine) & (j < lane));
+      // A batch already in that order (equal lengths included) needs no ranking.
+      const int next = __shfl_down(mine, 1);
+      int rank = lane;
+      if (!__all(lane + 1 >= B || mine >= next)) {
+        // Unique keys (length, then lower index first; lengths below 2^25): rank = keys
+        // above this one.
+        const int key = lane < B ? mine * kWave + (kWave - 1 - lane) : -1;
+        rank = 0;
+        for (int j = 0; j < B; ++j) rank += __builtin_amdgcn_readlane(key, j) > key;
       }
       const int ra = blockIdx.y, rb = B - 1 - ra;
       pair_a = __builtin_ctzll(__ballot(lane < B && rank == ra));
       pair_b = rb != ra ? __builtin_ctzll(__ballot(lane < B && rank == rb)) : -1;
+      len_a = __builtin_amdgcn_readlane(mine, pair_a);
+      len_b = pair_b >= 0 ? __builtin_amdgcn_readlane(mine, pair_b) : 0;
       // The waves take equal shares of the two sequences' blocks laid end to end; at
       // most one wave's share straddles both, and it walks them one after the other.
       const int bmask = (1 << a.lbs) - 1;
-      const int n_a = (a.lens[pair_a] + bmask) >> a.lbs;
-      const int n_b = pair_b >= 0 ? (a.lens[pair_b] + bmask) >> a.lbs : 0;
-      const int share = (n_a + n_b + a.wpg - 1) / a.wpg;
+      n_a = (len_a + bmask) >> a.lbs;
+      const int n_b = (len_b + bmask) >> a.lbs;
+      share = (n_a + n_b + a.wpg - 1) / a.wpg;
       const int lo = min(wave * share, n_a + n_b), hi = min(lo + share, n_a + n_b);
       nseg = 0;
       if (lo < n_a) {
@@ -306,7 +310,7 @@ void paged_attend_kernel(const AttendArgs a) {
       seq = pair_a;
     }
     split = blockIdx.z;
-    ctx = a.lens[seq];
+    ctx = a.by_length ? len_a : a.lens[seq];
     qrow = seq * a.q_sb;
     orow = seq * a.o_sb;
   }
@@ -323,11 +327,10 @@ void paged_attend_kernel(const AttendArgs a) {
 
   TokenState<T, D, HT> st;
   __shared__ PairSlots<T, D, HT> pslots;
-  if (pair && lane < 2) pslots.tag[wave][lane] = -1;
   for (int sgi = 0; sgi < nseg; ++sgi) {
   if (pair) {
     seq = seg_seq[sgi];
-    ctx = a.lens[seq];
+    ctx = seq == pair_a ? len_a : len_b;
     qrow = seq * a.q_sb;
     first = seg_first[sgi];
     last = seg_last[sgi];
@@ -435,28 +438,30 @@ void paged_attend_kernel(const AttendArgs a) {
   }
 
   merge_token_lanes(st);
-  if (pair) park_state(pslots, st, wave, sgi, seq == pair_a ? 0 : 1, tl == 0 ? c : -1);
+  if (pair) park_state(pslots, st, wave, sgi, tl == 0 ? c : -1);
   }  // segments
   if constexpr (!PREFILL) {
     if (pair) {
       __syncthreads();
+      // Wave w walked blocks [w * share, (w + 1) * share) of the two sequences laid end
+      // to end: the first sequence's states are slot 0 of waves 0 .. wa - 1; the
+      // second's are in waves wb .. W - 1, in slot 1 of a wave that also walked the first.
       const int W = a.wpg;
+      const int wa = min((n_a + share - 1) / share, W), wb = n_a / share;
       const int parts = pair_b >= 0 ? 2 : 1;
       for (int t = threadIdx.x; t < parts * HT * D; t += W * kWave) {
         const int pi = t / (HT * D);
         const int g = (t % (HT * D)) / D, d = t % D;
+        const int w0 = pi ? wb : 0, w1 = pi ? W : wa;
         float mm = kNoMax;
-        for (int w = 0; w < W; ++w)
-          for (int sl = 0; sl < 2; ++sl)
-            if (pslots.tag[w][sl] == pi) mm = fmaxf(mm, pslots.m[w][sl][g]);
+        for (int w = w0; w < w1; ++w) mm = fmaxf(mm, pslots.m[w][pi && w * share < n_a][g]);
         float den = 0.f, num = 0.f;
-        for (int w = 0; w < W; ++w)
-          for (int sl = 0; sl < 2; ++sl)
-            if (pslots.tag[w][sl] == pi) {
-              const float f = fast_exp2(pslots.m[w][sl][g] - mm);
-              den = fmaf(f, pslots.l[w][sl][g], den);
-              num = fmaf(f, pslots.acc[w][sl][g][d], num);
-            }
+        for (int w = w0; w < w1; ++w) {
+          const int sl = pi && w * share < n_a;
+          const float f = fast_exp2(pslots.m[w][sl][g] - mm);
+          den = fmaf(f, pslots.l[w][sl][g], den);
+          num = fmaf(f, pslots.acc[w][sl][g][d], num);
+        }
         const int64_t row = static_cast<int64_t>(pi ? pair_b : pair_a) * a.o_sb;
         static_cast<T*>(a.out)[row + (h0 + g) * a.o_sh + d] = from_f32<T>(num / den);
       }
