@@ -266,6 +266,33 @@ def test_sequences_paired_by_length(batch: int, kind: str) -> None:
     assert_matches(out, want, torch.float16, f"B={batch} {kind}")
 
 
+def test_paired_sequences_of_2_to_the_25_tokens() -> None:
+    # Contexts of 2^25 tokens and more take the pair ranking's exact comparison (its
+    # packed keys hold shorter lengths only). Both long tables repeat block 0 (65,536
+    # slots), so each long context is that block's keys and values repeated 512 or 513
+    # times: equal weights per repeat, so the exact answer is attention over the block
+    # once. The short sequences live in block 1.
+    bs, hq, hkv, d, batch = 1 << 16, 16, 8, 128, 40
+    g = torch.Generator().manual_seed(25)
+    k = torch.randn(2 * bs, hkv, d, generator=g).half()
+    v = torch.randn(2 * bs, hkv, d, generator=g).half()
+    q = torch.randn(batch, hq, d, generator=g).half()
+    lens = [1 + (389 * b) % 1000 for b in range(batch)]
+    lens[3], lens[17] = 1 << 25, (1 << 25) + bs
+    tables = torch.ones(batch, 513, dtype=torch.int32)
+    tables[3, :512] = 0
+    tables[17, :] = 0
+    scale = d**-0.5
+    out = ha.launch_paged_decode_split(q.to(DEVICE), k.to(DEVICE), v.to(DEVICE), tables.to(DEVICE),
+                                       torch.tensor(lens, dtype=torch.int32, device=DEVICE), scale, bs,
+                                       num_splits=1)  # fmt: skip
+    once = torch.tensor([bs if n >= bs else n for n in lens], dtype=torch.int32)
+    first = torch.where(torch.tensor(lens) >= bs, 0, 1).to(torch.int32)[:, None]
+    want = ref.decode_ref(q.float(), k.float(), v.float(), first, once, scale, bs)
+    assert torch.isfinite(out).all()
+    assert_matches(out, want, torch.float16, "contexts of 2^25 tokens")
+
+
 @pytest.mark.parametrize("splits", [2, 3, 4])
 def test_partials_and_combine_at_small_split_counts(splits: int) -> None:
     # launch_paged_decode_split runs up to 4 splits inside one workgroup; the C entry's

@@ -280,11 +280,17 @@ void paged_attend_kernel(const AttendArgs a) {
       const int next = __shfl_down(mine, 1);
       int rank = lane;
       if (!__all(lane + 1 >= B || mine >= next)) {
-        // Unique keys (length, then lower index first; lengths below 2^25): rank = keys
-        // above this one.
-        const int key = lane < B ? mine * kWave + (kWave - 1 - lane) : -1;
         rank = 0;
-        for (int j = 0; j < B; ++j) rank += __builtin_amdgcn_readlane(key, j) > key;
+        if (__all(mine < (1 << 25))) {
+          // Unique keys (length, then lower index first): rank = keys above this one.
+          const int key = lane < B ? mine * kWave + (kWave - 1 - lane) : -1;
+          for (int j = 0; j < B; ++j) rank += __builtin_amdgcn_readlane(key, j) > key;
+        } else {
+          for (int j = 0; j < B; ++j) {
+            const int other = __builtin_amdgcn_readlane(mine, j);
+            rank += (other > mine) | ((other == mine) & (j < lane));
+          }
+        }
       }
       const int ra = blockIdx.y, rb = B - 1 - ra;
       pair_a = __builtin_ctzll(__ballot(lane < B && rank == ra));
