@@ -133,6 +133,27 @@ def loop_ms(fn, iters: int = 20, warmup: int = 3) -> float:
     return a.elapsed_time(b) / iters
 
 
+def graph_ms(fn, launches: int = 20, replays: int = 10) -> float:
+    """Mean time of one ``fn`` launch, from a captured graph of ``launches`` of them
+    replayed ``replays`` times: the kernels' own rate, without the Python call overhead
+    that bounds a loop of eager calls to microsecond kernels."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(launches):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / (replays * launches)
+
+
 def cpu_baseline(case, splits: int, budget_s: float = 15.0) -> dict:
     """The oracle (PyTorch reference path restated) on this host, over the same 64 x 4096
     workload, repeated until ``budget_s`` of work (at least once)."""
@@ -226,15 +247,22 @@ def extra_measurements() -> dict:
                                          "mfma_frac": round(f1 / ms / 1e9 / FP16_PEAK_TFLOPS, 4)}
     # Config 4: fused RMSNorm + q/k norm + RoPE + KV write, T=4096.
     f = fused_case(device=dev, sentinel=False)
-    ms_r = loop_ms(lambda: rms_norm_rows(f.x, f.norm_w, f.eps), 200, 20)
-    ms_q = loop_ms(lambda: qk_norm_rope_store(f.q, f.k, f.v, f.q_w, f.k_w, f.cos, f.sin, f.slots,
-                                              f.k_cache, f.v_cache, f.eps), 200, 20)  # fmt: skip
+    def rms() -> None:
+        rms_norm_rows(f.x, f.norm_w, f.eps)
+
+    def qk() -> None:
+        qk_norm_rope_store(f.q, f.k, f.v, f.q_w, f.k_w, f.cos, f.sin, f.slots, f.k_cache, f.v_cache, f.eps)
+
+    eager_r, eager_q = loop_ms(rms, 200, 20), loop_ms(qk, 200, 20)
+    ms_r, ms_q = graph_ms(rms), graph_ms(qk)
     t = 4096
     b_r, b_q = t * 1024 * 2 * 2, t * 16904
     res["fused_t4096"] = {
         "rms_norm_rows_us": round(ms_r * 1e3, 2), "rms_GB/s": round(b_r / ms_r / 1e6, 1),
         "qk_norm_rope_store_us": round(ms_q * 1e3, 2), "qk_GB/s": round(b_q / ms_q / 1e6, 1),
-        "bytes": b_r + b_q}  # fmt: skip
+        "bytes": b_r + b_q, "timing": "graph replay of 20 launches",
+        "eager_call_us": {"rms_norm_rows": round(eager_r * 1e3, 2),
+                          "qk_norm_rope_store": round(eager_q * 1e3, 2)}}  # fmt: skip
     # Config 5: the 28-layer decode step.
     res["decode_step_28l_b64"] = decode_step_28l()
     return res

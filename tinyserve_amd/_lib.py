@@ -80,12 +80,17 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+_fns: dict[str, object] = {}
+
+
 def call(name: str, *args: object) -> None:
     """Call entry point ``name``; raise on a non-zero status."""
-    lib = load()
-    rc = getattr(lib, name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load(), name)
+    rc = fn(*args)
     if rc != 0:
-        msg = lib.ts_strerror(rc).decode()
+        msg = load().ts_strerror(rc).decode()
         if rc < 0:
             raise ValueError(f"{name}: {msg}")
         raise RuntimeError(f"{name}: HIP error {rc}: {msg}")
@@ -98,23 +103,27 @@ def dtype_code(t: torch.Tensor) -> int:
         raise ValueError(f"unsupported dtype {t.dtype}: float32, float16 or bfloat16") from None
 
 
-def require_device(*tensors: torch.Tensor) -> torch.device:
-    """The common HIP device of ``tensors``; RuntimeError for CPU tensors (no fallback)."""
-    dev = tensors[0].device
+def require_device(*tensors: torch.Tensor) -> int:
+    """Index of the common HIP device of ``tensors``; RuntimeError for CPU tensors (no
+    fallback)."""
+    idx = -1
     for t in tensors:
-        if t.device.type != "cuda":
+        if not t.is_cuda:
             raise RuntimeError(
                 "tinyserve_amd kernels run on a HIP device only (no CPU fallback); "
                 f"got a tensor on {t.device}"
             )
-        if t.device != dev:
-            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
-    return dev
+        i = t.get_device()
+        if idx < 0:
+            idx = i
+        elif i != idx:
+            raise ValueError(f"tensors on different devices: cuda:{idx} and cuda:{i}")
+    return idx
 
 
-def stream_of(dev: torch.device) -> int:
-    """Handle of torch's current stream on ``dev`` (the kernels launch there)."""
-    return torch.cuda.current_stream(dev).cuda_stream
+def stream_of(dev: int) -> int:
+    """Handle of torch's current stream on device ``dev`` (the kernels launch there)."""
+    return torch._C._cuda_getCurrentRawStream(dev)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

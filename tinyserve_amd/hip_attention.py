@@ -153,9 +153,9 @@ def _launch(
                   None, None, None, b, hq, hkv, d, block_size, *strides, 1, head_tile,
                   scale, dt, stream)  # fmt: skip
         return out
-    m = torch.empty((b, hq, splits), dtype=torch.float32, device=dev)
+    m = torch.empty((b, hq, splits), dtype=torch.float32, device=q.device)
     l = torch.empty_like(m)  # noqa: E741
-    acc = torch.empty((b, hq, splits, d), dtype=torch.float32, device=dev)
+    acc = torch.empty((b, hq, splits, d), dtype=torch.float32, device=q.device)
     _lib.call("ts_decode_split", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
               block_tables.data_ptr(), context_lens.data_ptr(), out.data_ptr(),
               m.data_ptr(), l.data_ptr(), acc.data_ptr(), b, hq, hkv, d, block_size,
