@@ -9,7 +9,7 @@ Per layer, on the flat ``[N]`` rows of a ``DecodeInputs`` (step_inputs.py):
     qkv  = h @ W_qkv^T                                             GEMM (hipBLASLt via torch)
     q    = qk_norm_rope_store(q, k, v, ...) -> K/V cache at slots  HIP  (fused.hip)
     attn = paged decode attention over the block tables            HIP  (decode.hip)
-    x   += attn @ W_o^T
+    x   += attn @ W_o^T                                             GEMM, residual add in it
     h    = rms_norm_rows(x, post_attention_layernorm)              HIP
     x   += (silu(gate) * up) @ W_down^T, [gate | up] = h @ W_gate_up^T
 
@@ -155,10 +155,11 @@ class DecodeStep:
             w[p + "self_attn.k_norm.weight"], cos, sin, slots, self.pool.k[i],
             self.pool.v[i], s.rms_norm_eps)  # fmt: skip
         attn = attend(i, q)
-        x = x + F.linear(attn.reshape(n, s.q_size), w[p + "self_attn.o_proj.weight"])
+        # Residual adds ride in the GEMMs (beta = 1): one launch each instead of two.
+        x = torch.addmm(x, attn.reshape(n, s.q_size), w[p + "self_attn.o_proj.weight"].t())
         h = hip_fused.rms_norm_rows(x, w[p + "post_attention_layernorm.weight"], s.rms_norm_eps)
         gate, up = F.linear(h, w[p + "mlp.gate_up_proj.weight"]).chunk(2, dim=1)
-        return x + F.linear(F.silu(gate) * up, w[p + "mlp.down_proj.weight"])
+        return torch.addmm(x, F.silu(gate) * up, w[p + "mlp.down_proj.weight"].t())
 
     def _run(self, token_ids: torch.Tensor, positions: torch.Tensor, slots: torch.Tensor,
              attend: Callable[[int, torch.Tensor], torch.Tensor],
