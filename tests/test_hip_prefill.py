@@ -153,13 +153,14 @@ def test_baseline_config_3(dtype: torch.dtype) -> None:
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_both_workgroup_shapes(dtype: torch.dtype) -> None:
-    # The library runs 8-wave workgroups (128 queries x 2 heads, 3-stage ring) when the
-    # launch has at least two of them per CU, else 4-wave ones (64 queries x 2 heads,
-    # 2-stage ring, two per CU). At Qwen3 shapes 4 prompts of up to 2048 tokens make 512
-    # 8-wave workgroups (8-wave shape on 256 CUs); 3 make 384 (4-wave shape).
-    # 16 prompts of up to 512 tokens (mean under 1280) run the 4-wave, 32-key shape at
-    # three per CU.
-    for lens in ([2048, 1999, 1100, 700], [2048, 1500, 64], [512] * 15 + [77]):
+    # The library picks the workgroup shape from the 8-wave grid (wg8 workgroups of 128
+    # queries x 2 heads) at Qwen3 shapes on 256 CUs: 3 prompts of up to 2048 tokens make
+    # 256 (under 1.5 per CU: 4 waves, 64-key tiles, two per CU); 4 prompts make 512 and 16
+    # prompts of up to 512 tokens 512 (4 waves, 32-key tiles, three per CU); 24 prompts
+    # of up to 1408 tokens make 2112, over 8 per CU with a mean above 1280 new tokens
+    # (8 waves, 64-key tiles, many query tiles per sequence).
+    for lens in ([2048, 1999, 1100, 700], [2048, 1500, 64], [512] * 15 + [77],
+                 [1300 + (37 * i) % 109 for i in range(23)] + [1408]):  # fmt: skip
         c = prefill_case([(0, n) for n in lens], 16, 8, 128, 16, dtype, seed=len(lens))
         check(c, run(c))
 
@@ -168,9 +169,9 @@ def test_both_workgroup_shapes(dtype: torch.dtype) -> None:
 @pytest.mark.parametrize("shape", [(16, 8, 128), (8, 2, 64)])
 def test_every_gather_path_on_every_workgroup_shape(block_size: int, shape: tuple[int, int, int]) -> None:
     # Each launch below runs one of the three workgroup shapes (one prompt: 4 waves,
-    # 64-key tiles; 16 prompts of 512: 4 waves, 32-key tiles; 4 x 2048: 8 waves), with
-    # prefix hits so that tiles start mid-block, at every block size.
-    for specs in ([(70, 300)], [(33, 512)] * 15 + [(5, 77)], [(100, 2048)] * 4):
+    # 64-key tiles; 16 prompts of 512: 4 waves, 32-key tiles; 4 chunks of 128 new tokens:
+    # 8 waves), with prefix hits so that tiles start mid-block, at every block size.
+    for specs in ([(70, 300)], [(33, 512)] * 15 + [(5, 77)], [(100 + 300 * i, 128) for i in range(4)]):
         c = prefill_case(specs, *shape, block_size, torch.float16, seed=block_size)
         check(c, run(c))
 

@@ -30,11 +30,12 @@
 // share one XCD's L2, where its K/V blocks are re-read by every query tile.
 //
 // Three shapes: 8 waves with a 3-stage ring of 64-key tiles (one workgroup per CU, 98 KB
-// of LDS, two waves per SIMD); for launches with too few query tiles to fill the chip
-// that way, 4 waves with a 2-stage ring (66 KB: two workgroups per CU, half the queries
-// per workgroup); and for mid-size launches of short prompts, 4 waves over 32-key tiles
-// (a 2-stage ring of 34 KB, 157 VGPRs: three workgroups, so three waves, per SIMD), whose
-// extra wave per SIMD and finer key tiles outweigh the doubled barriers there.
+// of LDS, two waves per SIMD) for large launches and prefix-hit chunks; for launches with
+// too few query tiles to fill the chip that way, 4 waves with a 2-stage ring (66 KB: two
+// workgroups per CU, half the queries per workgroup); and for mid-size launches, 4 waves
+// over 32-key tiles (a 2-stage ring of 34 KB, 157 VGPRs: three workgroups, so three
+// waves, per SIMD), whose extra wave per SIMD and finer key tiles outweigh the doubled
+// barriers there.
 //
 // MFMA formulation (v_mfma_f32_32x32x16_{f16,bf16}). Scores are computed transposed,
 // S^T[key, query] = K . Q^T, with K as the A operand (one 16-byte LDS read per lane) and
@@ -665,10 +666,11 @@ static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows,
 
 // Which of the three workgroup shapes a launch runs (see the header comment). wg8 is the
 // 8-wave grid. Measured at Qwen3 shapes: chunks of at most 128 new tokens (prefix hits)
-// run the 8-wave shape (+2.5-9.5%); small grids (one to two prompts) the 4-wave, 64-key
-// shape at two per CU; mid-size grids of short prompts (mean new tokens per sequence up
-// to 1280: 8-32 mixed prompts, 16 x 512, 64 x 256) the 4-wave, 32-key shape at three per
-// CU (+5-14%); long prompts and large grids the 8-wave shape.
+// run the 8-wave shape (+2.5-9.5%); grids under 1.5 8-wave workgroups per CU (one or two
+// long prompts) the 4-wave, 64-key shape at two per CU; grids of 1.5 to 8 per CU (3-16
+// prompts of 2048, 1-4 of 4096-8192: +1-10%), and of up to 16 per CU when the mean new
+// tokens per sequence is at most 1280 (8-32 mixed prompts, 16 x 512, 64 x 256: +5-14%),
+// the 4-wave, 32-key shape at three per CU; larger grids the 8-wave shape.
 enum class PrefillShape { kW8, kW4, kW4Short };
 
 static PrefillShape prefill_shape(int R, int group, int Hkv, int max_q_len, int64_t n_rows) {
@@ -680,9 +682,9 @@ static PrefillShape prefill_shape(int R, int group, int Hkv, int max_q_len, int6
   // Up to 128 new tokens per sequence: one 8-wave query tile holds a whole sequence, so
   // its K/V (the whole cached prefix) is read once per kv head, not once per 64 queries.
   if (max_q_len <= 128) return PrefillShape::kW8;
+  if (2 * wg8 < 3 * cus) return PrefillShape::kW4;
   const bool short_mean = n_rows > 0 && n_rows <= 1280 * static_cast<int64_t>(R);
-  if (short_mean && wg8 >= 2 * cus && wg8 <= 16 * cus) return PrefillShape::kW4Short;
-  if (wg8 < 2 * cus) return PrefillShape::kW4;
+  if (wg8 <= 8 * cus || (short_mean && wg8 <= 16 * cus)) return PrefillShape::kW4Short;
   return PrefillShape::kW8;
 }
 
