@@ -629,9 +629,6 @@ extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v
   // workgroups. A batch of equal contexts runs exactly as before (two waves per
   // sequence); one of mixed lengths no longer waits on its longest sequences.
   int by_length = B <= kWave && B >= 2 && splits == 1 && wpg == 2 ? 1 : 0;
-#ifdef DEC_ENV
-  if (getenv("TS_BYLEN")) by_length = by_length && atoi(getenv("TS_BYLEN"));
-#endif
   if (by_length) wpg = kMaxWavesPerGroup;
   AttendArgs a{q, k_cache, v_cache, block_tables, context_lens, out, m, l, acc, nullptr,
                nullptr, Hq, group, ilog2(block_size), splits, wpg, 0, by_length, B, q_stride_b,
