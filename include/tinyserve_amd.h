@@ -70,7 +70,8 @@ int ts_decode_split(const void* q, const void* k_cache, const void* v_cache,
 
 /*
  * The split-K combine pass: out[b, h] = sum_s w_s acc_s / sum_s w_s l_s with
- * w_s = 2^(m_s - max_s m_s); an empty range (m = -inf, l = 0) weighs 0.
+ * w_s = 2^(m_s - max_s m_s); an empty range (m = -inf, l = 0) weighs 0. Head dims up to
+ * 256 (TS_EUNSUPPORTED above), any number of splits.
  * Replaces _merge_splits_kernel (triton_attention.py:299-327).
  */
 int ts_decode_combine(const float* m, const float* l, const float* acc, void* out, int B,

@@ -302,3 +302,20 @@ def test_partials_and_combine_at_small_split_counts(splits: int) -> None:
     g = on_gpu(c)
     out = ha._launch(*g.args(), g.scale, g.block_size, splits, 0)
     assert_matches(out, want, torch.float16, f"splits={splits}")
+
+
+@pytest.mark.parametrize("splits", [9, 64, 65, 130])
+@pytest.mark.parametrize("head_dim,dtype", [(128, torch.float16), (64, torch.float32), (256, torch.bfloat16),
+                                            (8, torch.float16)])  # fmt: skip
+def test_combine_over_many_splits(splits: int, head_dim: int, dtype: torch.dtype) -> None:
+    # The combine reduces the splits' maxima and denominators over the lanes of a wave, 64
+    # splits at a time, and reads 8 splits' partials at once: split counts past one and two
+    # rounds of 64, many of them empty (m = -inf, l = 0) for the short sequences, and head
+    # dims of one, two and four elements per lane.
+    c = decode_case([17, 3000, 33, 1, 700], num_q_heads=8, num_kv_heads=4, head_dim=head_dim, dtype=dtype,
+                    seed=splits)  # fmt: skip
+    want = oracle32(c)
+    g = on_gpu(c)
+    out = ha._launch(*g.args(), g.scale, g.block_size, splits, 0)
+    assert torch.isfinite(out).all()
+    assert_matches(out, want, dtype, f"splits={splits} D={head_dim}")

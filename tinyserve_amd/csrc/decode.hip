@@ -512,24 +512,67 @@ void paged_attend_kernel(const AttendArgs a) {
   }
 }
 
-// The split-K combine: one wave per (sequence, query head).
-template <typename T>
+// Max over the 64 lanes of a wave; every lane ends with it.
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, xor_lane<1>(x));
+  x = fmaxf(x, xor_lane<2>(x));
+  x = fmaxf(x, xor_lane<4>(x));
+  x = fmaxf(x, xor_lane<8>(x));
+  x = fmaxf(x, xor_lane<16>(x));
+  return halves_max(x);
+}
+
+// The split-K combine: one wave per (sequence, query head). Lane s holds split s's
+// maximum and denominator (64 splits at a time) and the wave reduces them; then each lane
+// owns output elements lane + 64 e and issues the partial-sum loads of 8 splits at once
+// before accumulating them, so a (sequence, head) waits on memory a few times, not once
+// per split and element.
+template <typename T, int ED>
 __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ m,
                                                      const float* __restrict__ l,
                                                      const float* __restrict__ acc, T* out,
                                                      int Hq, int D, int64_t o_sb, int64_t o_sh,
                                                      int splits) {
+  constexpr int kU = 8;  // splits whose loads are in flight together
+  const int lane = threadIdx.x;
   const int b = blockIdx.x, h = blockIdx.y;
   const int64_t base = (static_cast<int64_t>(b) * Hq + h) * splits;
   float mmax = -INFINITY;
-  for (int s = 0; s < splits; ++s) mmax = fmaxf(mmax, m[base + s]);
+  for (int s0 = 0; s0 < splits; s0 += kWave)
+    if (s0 + lane < splits) mmax = fmaxf(mmax, m[base + s0 + lane]);
+  mmax = wave_max(mmax);
   float den = 0.f;
-  for (int s = 0; s < splits; ++s) den += fast_exp2(m[base + s] - mmax) * l[base + s];
+  float num[ED];
+#pragma unroll
+  for (int e = 0; e < ED; ++e) num[e] = 0.f;
+  for (int s0 = 0; s0 < splits; s0 += kWave) {
+    const bool mine = s0 + lane < splits;
+    const float wgt = mine ? fast_exp2(m[base + s0 + lane] - mmax) : 0.f;
+    if (mine) den = fmaf(wgt, l[base + s0 + lane], den);
+    const int n = min(kWave, splits - s0);
+    for (int j = 0; j < n; j += kU) {
+      float x[kU][ED];
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+#pragma unroll
+        for (int e = 0; e < ED; ++e) {
+          const int d = lane + kWave * e;
+          x[u][e] = j + u < n && d < D ? acc[(base + s0 + j + u) * D + d] : 0.f;
+        }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const float w = __shfl(wgt, j + u);  // 0 past the last split
+#pragma unroll
+        for (int e = 0; e < ED; ++e) num[e] = fmaf(w, x[u][e], num[e]);
+      }
+    }
+  }
+  den = group_sum<kWave>(den);
   T* op = out + b * o_sb + h * o_sh;
-  for (int d = threadIdx.x; d < D; d += kWave) {
-    float num = 0.f;
-    for (int s = 0; s < splits; ++s) num += fast_exp2(m[base + s] - mmax) * acc[(base + s) * D + d];
-    op[d] = from_f32<T>(num / den);
+#pragma unroll
+  for (int e = 0; e < ED; ++e) {
+    const int d = lane + kWave * e;
+    if (d < D) op[d] = from_f32<T>(num[e] / den);
   }
 }
 
@@ -599,6 +642,20 @@ int prefill_rows_generic(const void* q, const void* k, const void* v, void* out,
   return dispatch_attend<true>(a, dtype, D, ht, grid, stream);
 }
 
+template <typename T>
+static int launch_combine(const float* m, const float* l, const float* acc, T* out, int B, int Hq,
+                          int D, int64_t o_sb, int64_t o_sh, int splits, hipStream_t st) {
+  const dim3 grid(B, Hq);
+  if (D <= kWave) {
+    hipLaunchKernelGGL((combine_kernel<T, 1>), grid, dim3(kWave), 0, st, m, l, acc, out, Hq, D, o_sb, o_sh, splits);
+  } else if (D <= 2 * kWave) {
+    hipLaunchKernelGGL((combine_kernel<T, 2>), grid, dim3(kWave), 0, st, m, l, acc, out, Hq, D, o_sb, o_sh, splits);
+  } else {
+    hipLaunchKernelGGL((combine_kernel<T, 4>), grid, dim3(kWave), 0, st, m, l, acc, out, Hq, D, o_sb, o_sh, splits);
+  }
+  return launch_status();
+}
+
 }  // namespace ts
 
 using namespace ts;
@@ -643,24 +700,14 @@ extern "C" int ts_decode_combine(const float* m, const float* l, const float* ac
                                  int splits, int dtype, void* stream) {
   if (B < 0 || Hq <= 0 || D <= 0 || splits < 1) return TS_EINVAL;
   if (B == 0) return 0;
-  dim3 grid(B, Hq);
+  if (D > 4 * kWave) return TS_EUNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case TS_F32:
-      hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(kWave), 0, st, m, l, acc,
-                         static_cast<float*>(out), Hq, D, o_stride_b, o_stride_h, splits);
-      break;
-    case TS_F16:
-      hipLaunchKernelGGL(combine_kernel<f16>, grid, dim3(kWave), 0, st, m, l, acc,
-                         static_cast<f16*>(out), Hq, D, o_stride_b, o_stride_h, splits);
-      break;
-    case TS_BF16:
-      hipLaunchKernelGGL(combine_kernel<bf16>, grid, dim3(kWave), 0, st, m, l, acc,
-                         static_cast<bf16*>(out), Hq, D, o_stride_b, o_stride_h, splits);
-      break;
+    case TS_F32: return launch_combine<float>(m, l, acc, static_cast<float*>(out), B, Hq, D, o_stride_b, o_stride_h, splits, st);
+    case TS_F16: return launch_combine<f16>(m, l, acc, static_cast<f16*>(out), B, Hq, D, o_stride_b, o_stride_h, splits, st);
+    case TS_BF16: return launch_combine<bf16>(m, l, acc, static_cast<bf16*>(out), B, Hq, D, o_stride_b, o_stride_h, splits, st);
     default: return TS_EUNSUPPORTED;
   }
-  return launch_status();
 }
 
 extern "C" int ts_version(void) { return (0 << 16) | 1; }
