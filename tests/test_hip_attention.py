@@ -293,6 +293,25 @@ def test_paired_sequences_of_2_to_the_25_tokens() -> None:
     assert_matches(out, want, torch.float16, "contexts of 2^25 tokens")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("batch,splits,head_dim", [(256, 1, 128), (64, 16, 128), (300, 1, 64), (40, 9, 256)])
+def test_launches_of_several_rounds(batch: int, splits: int, head_dim: int, dtype: torch.dtype) -> None:
+    # Grids of at least 8 waves per CU (two rounds of one wave per SIMD; 2048 waves on 256
+    # CUs) run the kernel's light register budget: 32 bytes of a row per lane, two waves
+    # per SIMD. Here: 256 and 300 sequences at one split, 64 at the reference's 16 splits
+    # (HBM partials and the combine), 40 at 9 splits with D=256; the grouped and the
+    # per-head (head tile 1) launches.
+    lens = [1 + (211 * i) % 900 for i in range(batch)]
+    c = decode_case(lens, head_dim=head_dim, dtype=dtype, seed=batch + splits)
+    want = oracle32(c)
+    g = on_gpu(c)
+    out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, num_splits=splits)
+    assert torch.isfinite(out).all()
+    assert_matches(out, want, dtype, f"B={batch} splits={splits} D={head_dim}")
+    per_head = ha._launch(*g.args(), c.scale, c.block_size, splits, 1)
+    assert_matches(per_head, want, dtype, f"head tile 1, B={batch} splits={splits} D={head_dim}")
+
+
 @pytest.mark.parametrize("splits", [2, 3, 4])
 def test_partials_and_combine_at_small_split_counts(splits: int) -> None:
     # launch_paged_decode_split runs up to 4 splits inside one workgroup; the C entry's

@@ -17,8 +17,11 @@
 // workgroup of W = 1, 2 or 4 waves; wave w takes the w-th of W contiguous block ranges of
 // the split's range, and the W partial states are merged through LDS before anything is
 // written. This is split-K without HBM partials or a second launch: the library picks W
-// so that the grid holds about four waves per CU (the kernel needs more than 256 VGPRs,
-// so a SIMD runs one wave of it, and a CU wants four in flight to cover HBM latency).
+// so that the grid holds about four waves per CU (the kernel's heavy register budget
+// needs more than 256 VGPRs, so a SIMD runs one wave of it, and a CU wants four in
+// flight to cover HBM latency). Launches of two or more rounds of such waves (many
+// sequences, or many splits) take the light budget instead: 32 bytes per lane, two waves
+// per SIMD, so that one wave's start-up chain and merge hide under another's streaming.
 //
 // Length pairs. A batch of at most 64 sequences that would get two-wave workgroups is
 // run as pairs instead: workgroup y takes the sequences ranked y and B - 1 - y by
@@ -35,24 +38,26 @@
 // l = 2^(m1-m) l1 + 2^(m2-m) l2 (same for acc), the rule the combine pass uses too.
 #include "common.h"
 
-// Bytes of a head row each lane streams per token, and the occupancy the register
-// budget is sized for (waves per SIMD).
-#ifndef TS_DECODE_LANE_BYTES
-#define TS_DECODE_LANE_BYTES 64
-#endif
-#ifndef TS_DECODE_NBUF
-#define TS_DECODE_NBUF 3
-#endif
-#ifndef TS_DECODE_WAVES_PER_EU
-#define TS_DECODE_WAVES_PER_EU 1
-#endif
-
 namespace ts {
 
-template <typename T, int D>
+// Two register budgets. kHeavy: each lane streams 64 bytes of a head row per token, three
+// iterations in flight, one wave per SIMD (more than 256 VGPRs) -- for launches whose
+// waves all run in one round, where each wave must keep much in flight. kLight: 32 bytes
+// per lane, three in flight, two waves per SIMD -- for launches of several rounds, where
+// the second wave per SIMD hides each wave's start-up chain (lengths, block table, first
+// loads) and merge.
+enum Budget { kHeavy = 0, kLight = 1 };
+template <int B>
+struct BudgetOf {
+  static constexpr int kLaneBytes = B == kLight ? 32 : 64;
+  static constexpr int kNBuf = 3;
+  static constexpr int kWavesPerEU = B == kLight ? 2 : 1;
+};
+
+template <typename T, int D, int LB>
 struct RowShape {
   static constexpr int kRowBytes = D * static_cast<int>(sizeof(T));
-  static constexpr int kLaneBytes = TS_DECODE_LANE_BYTES;  // bytes of a row per lane
+  static constexpr int kLaneBytes = LB;  // bytes of a row per lane
   static constexpr int kLPT =
       kRowBytes <= kLaneBytes ? 1 : (kRowBytes / kLaneBytes > 64 ? 64 : kRowBytes / kLaneBytes);
   static constexpr int kE = D / kLPT;
@@ -114,18 +119,18 @@ __device__ __forceinline__ float dot16(const Pack16<float>& a, const Pack16<floa
   return s;
 }
 
-template <typename T, int D, int HT>
+template <typename T, int D, int HT, int LB>
 struct TokenState {
-  using S = RowShape<T, D>;
+  using S = RowShape<T, D, LB>;
   float m[HT];
   float l[HT];
   float acc[HT][S::kE];
 };
 
 // Merge the partial softmax states of lanes OFF apart (token lanes only: OFF >= LPT).
-template <int OFF, typename T, int D, int HT>
-__device__ __forceinline__ void merge_lanes(TokenState<T, D, HT>& st) {
-  using S = RowShape<T, D>;
+template <int OFF, typename T, int D, int HT, int LB>
+__device__ __forceinline__ void merge_lanes(TokenState<T, D, HT, LB>& st) {
+  using S = RowShape<T, D, LB>;
 #pragma unroll
   for (int g = 0; g < HT; ++g) {
     const float mo = xor_lane<OFF>(st.m[g]);
@@ -140,9 +145,9 @@ __device__ __forceinline__ void merge_lanes(TokenState<T, D, HT>& st) {
   }
 }
 
-template <typename T, int D, int HT>
-__device__ __forceinline__ void merge_token_lanes(TokenState<T, D, HT>& st) {
-  constexpr int L = RowShape<T, D>::kLPT;
+template <typename T, int D, int HT, int LB>
+__device__ __forceinline__ void merge_token_lanes(TokenState<T, D, HT, LB>& st) {
+  constexpr int L = RowShape<T, D, LB>::kLPT;
   if constexpr (L <= 1) merge_lanes<1>(st);
   if constexpr (L <= 2) merge_lanes<2>(st);
   if constexpr (L <= 4) merge_lanes<4>(st);
@@ -162,7 +167,7 @@ template <typename T, int D, int HT, typename State, typename Args>
 __device__ __forceinline__ void merge_group_waves(const Args& a, const State& st, int wave,
                                                   int c, int seq, int h0, int split,
                                                   int64_t orow) {
-  using S = RowShape<T, D>;
+  using S = typename State::S;
   constexpr int NV = S::kNV, VEC = S::kVec, LPT = S::kLPT;
   __shared__ float sm[kMaxWavesPerGroup][HT], sl[kMaxWavesPerGroup][HT];
   __shared__ float sacc[kMaxWavesPerGroup][HT][D];
@@ -220,7 +225,7 @@ struct PairSlots {
 template <typename T, int D, int HT, typename State>
 __device__ __forceinline__ void park_state(PairSlots<T, D, HT>& ps, const State& st, int wave,
                                            int slot, int c) {
-  using S = RowShape<T, D>;
+  using S = typename State::S;
   constexpr int NV = S::kNV, VEC = S::kVec, LPT = S::kLPT;
   if (c < 0) return;
 #pragma unroll
@@ -236,13 +241,14 @@ __device__ __forceinline__ void park_state(PairSlots<T, D, HT>& ps, const State&
   }
 }
 
-template <typename T, int D, int HT, bool PREFILL>
+template <typename T, int D, int HT, bool PREFILL, int BUDGET>
 __global__ __launch_bounds__(PREFILL ? kWave : kWave * kMaxWavesPerGroup)
-__attribute__((amdgpu_waves_per_eu(TS_DECODE_WAVES_PER_EU)))
+__attribute__((amdgpu_waves_per_eu(BudgetOf<BUDGET>::kWavesPerEU)))
 void paged_attend_kernel(const AttendArgs a) {
-  using S = RowShape<T, D>;
+  constexpr int LB = BudgetOf<BUDGET>::kLaneBytes;
+  using S = RowShape<T, D, LB>;
   constexpr int LPT = S::kLPT, NV = S::kNV, VEC = S::kVec, TPW = S::kTPW, E = S::kE;
-  constexpr int NBUF = TS_DECODE_NBUF;
+  constexpr int NBUF = BudgetOf<BUDGET>::kNBuf;
   const int lane = threadIdx.x % kWave;
   const int wave = PREFILL ? 0 : threadIdx.x / kWave;
   const int c = lane % LPT;
@@ -331,7 +337,7 @@ void paged_attend_kernel(const AttendArgs a) {
   if constexpr (!PREFILL) pair = a.by_length;
   if (!pair) seg_seq[0] = seq, seg_first[0] = first, seg_last[0] = last;
 
-  TokenState<T, D, HT> st;
+  TokenState<T, D, HT, LB> st;
   __shared__ PairSlots<T, D, HT> pslots;
   for (int sgi = 0; sgi < nseg; ++sgi) {
   if (pair) {
@@ -577,19 +583,27 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ m
 }
 
 template <typename T, int D, int HT, bool PREFILL>
-static int launch_attend(const AttendArgs& a, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, PREFILL>), grid, dim3(kWave * a.wpg), 0,
-                     stream, a);
+static int launch_attend(const AttendArgs& a, dim3 grid, bool light, hipStream_t stream) {
+  // Four query heads' state does not fit the light budget without spilling.
+  if constexpr (HT <= 2) {
+    if (light) {
+      hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, PREFILL, kLight>), grid,
+                         dim3(kWave * a.wpg), 0, stream, a);
+      return launch_status();
+    }
+  }
+  hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, PREFILL, kHeavy>), grid, dim3(kWave * a.wpg),
+                     0, stream, a);
   return launch_status();
 }
 
 template <typename T, bool PREFILL>
-static int dispatch_d(const AttendArgs& a, int D, int ht, dim3 grid, hipStream_t stream) {
+static int dispatch_d(const AttendArgs& a, int D, int ht, dim3 grid, bool light, hipStream_t stream) {
 #define TS_HT(DD)                                                           \
   switch (ht) {                                                             \
-    case 1: return launch_attend<T, DD, 1, PREFILL>(a, grid, stream);       \
-    case 2: return launch_attend<T, DD, 2, PREFILL>(a, grid, stream);       \
-    case 4: return launch_attend<T, DD, 4, PREFILL>(a, grid, stream);       \
+    case 1: return launch_attend<T, DD, 1, PREFILL>(a, grid, light, stream); \
+    case 2: return launch_attend<T, DD, 2, PREFILL>(a, grid, light, stream); \
+    case 4: return launch_attend<T, DD, 4, PREFILL>(a, grid, light, stream); \
     default: return TS_EUNSUPPORTED;                                        \
   }
   switch (D) {
@@ -608,10 +622,14 @@ static int dispatch_d(const AttendArgs& a, int D, int ht, dim3 grid, hipStream_t
 template <bool PREFILL>
 static int dispatch_attend(const AttendArgs& a, int dtype, int D, int ht, dim3 grid,
                            hipStream_t stream) {
+  // Launches of two or more rounds of one-wave-per-SIMD waves take the light budget
+  // (head tiles of up to two query heads).
+  const int64_t waves = static_cast<int64_t>(grid.x) * grid.y * grid.z * a.wpg;
+  const bool light = waves >= 8 * static_cast<int64_t>(compute_units());
   switch (dtype) {
-    case TS_F32: return dispatch_d<float, PREFILL>(a, D, ht, grid, stream);
-    case TS_F16: return dispatch_d<f16, PREFILL>(a, D, ht, grid, stream);
-    case TS_BF16: return dispatch_d<bf16, PREFILL>(a, D, ht, grid, stream);
+    case TS_F32: return dispatch_d<float, PREFILL>(a, D, ht, grid, light, stream);
+    case TS_F16: return dispatch_d<f16, PREFILL>(a, D, ht, grid, light, stream);
+    case TS_BF16: return dispatch_d<bf16, PREFILL>(a, D, ht, grid, light, stream);
     default: return TS_EUNSUPPORTED;
   }
 }
