@@ -63,7 +63,7 @@ def split_kernel_launch(c, splits: int, m, l, acc, out, stream: int) -> None:
               c.block_tables.data_ptr(), c.context_lens.data_ptr(), out.data_ptr(),
               m.data_ptr(), l.data_ptr(), acc.data_ptr(), q.shape[0], HQ, HKV, D, BS,
               q.stride(0), q.stride(1), out.stride(0), out.stride(1), k.stride(0), k.stride(1),
-              c.block_tables.stride(0), splits, 0, c.scale, 1, stream)  # fmt: skip
+              c.block_tables.stride(0), c.block_tables.shape[1], splits, 0, c.scale, 1, stream)  # fmt: skip
 
 
 def combine_launch(splits: int, m, l, acc, out, stream: int) -> None:

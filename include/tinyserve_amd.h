@@ -59,14 +59,20 @@ const char* ts_strerror(int code);
  * writes its fp32 partial to m, l [B, Hq, splits] and acc [B, Hq, splits, D]
  * (contiguous, part index (b * Hq + h) * splits + split); `out` is not touched, and
  * ts_decode_combine finishes the result. m is stored in base-2 units (log2 e * max score).
+ *
+ * max_blocks: the width of block_tables (entries per row the caller filled, so every
+ * context is at most max_blocks * block_size), or 0 if unknown. It only picks the
+ * kernel's register budget (short walks per wave run two waves per SIMD); nothing is
+ * read by it, and a wrong value costs speed, never correctness. (The reference passes
+ * the table to Triton and has no such argument.)
  */
 int ts_decode_split(const void* q, const void* k_cache, const void* v_cache,
                     const int32_t* block_tables, const int32_t* context_lens, void* out,
                     float* m, float* l, float* acc, int B, int Hq, int Hkv, int D,
                     int block_size, int64_t q_stride_b, int64_t q_stride_h,
                     int64_t o_stride_b, int64_t o_stride_h, int64_t k_stride_slot,
-                    int64_t k_stride_head, int64_t bt_stride, int splits, int head_tile,
-                    float scale, int dtype, void* stream);
+                    int64_t k_stride_head, int64_t bt_stride, int max_blocks, int splits,
+                    int head_tile, float scale, int dtype, void* stream);
 
 /*
  * The split-K combine pass: out[b, h] = sum_s w_s acc_s / sum_s w_s l_s with

@@ -147,7 +147,7 @@ def test_every_tile_gives_the_same_result(tile: tuple[int, int], splits: int) ->
     assert_matches(grouped, want, torch.float32)
 
 
-WIDTHS = [1, 2, 9, 16, 32]
+WIDTHS = [1, 2, 9, 16, 32, 600]
 
 
 def widened(tables: torch.Tensor, width: int) -> torch.Tensor:
@@ -291,6 +291,25 @@ def test_paired_sequences_of_2_to_the_25_tokens() -> None:
     want = ref.decode_ref(q.float(), k.float(), v.float(), first, once, scale, bs)
     assert torch.isfinite(out).all()
     assert_matches(out, want, torch.float16, "contexts of 2^25 tokens")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("batch,splits", [(64, 1), (45, 1), (32, 4), (4, 1), (8, 8)])
+def test_both_register_budgets(batch: int, splits: int, dtype: torch.dtype) -> None:
+    # The table width bounds the tokens a wave walks; up to 512 of them the kernel runs
+    # its light budget (two waves per SIMD), else the heavy one. The same sequences
+    # through their own narrow table and through one widened to 2000 blocks give the
+    # reference either way: length pairs (64, 45), in-workgroup splits (32 x 4), a
+    # small batch, and HBM splits with the combine (8 x 8).
+    lens = [1 + (389 * i) % 300 for i in range(batch)]
+    c = decode_case(lens, dtype=dtype, seed=batch)
+    want = oracle32(c)
+    g = on_gpu(c)
+    for w in (g.block_tables.shape[1], 2000):
+        tables = widened(g.block_tables, w)
+        out = ha.launch_paged_decode_split(g.q, g.k_cache, g.v_cache, tables, g.context_lens, c.scale,
+                                           c.block_size, num_splits=splits)  # fmt: skip
+        assert_matches(out, want, dtype, f"width {w}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])

@@ -54,16 +54,16 @@ def test_c_abi_rejects_bad_sizes_before_any_launch(lib: ctypes.CDLL) -> None:
     # library returns TS_EINVAL without launching (null pointers are never touched).
     null = None
     strides = (0,) * 7
-    assert lib.ts_decode_split(*([null] * 9), 1, 6, 4, 32, 16, *strides, 1, 0, 1.0, 0, null) == -1
-    assert lib.ts_decode_split(*([null] * 9), 1, 4, 2, 32, 12, *strides, 1, 0, 1.0, 0, null) == -1
-    assert lib.ts_decode_split(*([null] * 9), 1, 4, 2, 32, 16, *strides, 0, 0, 1.0, 0, null) == -1
+    assert lib.ts_decode_split(*([null] * 9), 1, 6, 4, 32, 16, *strides, 0, 1, 0, 1.0, 0, null) == -1
+    assert lib.ts_decode_split(*([null] * 9), 1, 4, 2, 32, 12, *strides, 0, 1, 0, 1.0, 0, null) == -1
+    assert lib.ts_decode_split(*([null] * 9), 1, 4, 2, 32, 16, *strides, 0, 0, 0, 1.0, 0, null) == -1
     # splits > 1 needs the partial buffers
-    assert lib.ts_decode_split(*([null] * 9), 1, 4, 2, 32, 16, *strides, 2, 0, 1.0, 0, null) == -1
+    assert lib.ts_decode_split(*([null] * 9), 1, 4, 2, 32, 16, *strides, 0, 2, 0, 1.0, 0, null) == -1
     assert lib.ts_prefill_varlen(*([null] * 8), 1, 12, 4, 32, 16, 4, 0, *strides, 1.0, 0, null) == -1
     assert lib.ts_rms_norm_rows(null, null, null, 4, 0, 0, 0, 1e-6, 0, null) == -1
     assert lib.ts_qk_norm_rope_store(*([null] * 11), 1, 4, 2, 12, *([0] * 11), 1e-6, 0, 0, null) == -1
     # empty batches launch nothing and succeed
-    assert lib.ts_decode_split(*([null] * 9), 0, 4, 2, 32, 16, *strides, 1, 0, 1.0, 0, null) == 0
+    assert lib.ts_decode_split(*([null] * 9), 0, 4, 2, 32, 16, *strides, 0, 1, 0, 1.0, 0, null) == 0
     assert lib.ts_rms_norm_rows(null, null, null, 0, 16, 16, 16, 1e-6, 1, null) == 0
 
 

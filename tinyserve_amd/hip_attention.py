@@ -147,10 +147,11 @@ def _launch(
     dt = _lib.dtype_code(q)
     strides = (q.stride(0), q.stride(1), out.stride(0), out.stride(1),
                k_cache.stride(0), k_cache.stride(1), block_tables.stride(0))  # fmt: skip
+    width = block_tables.shape[1]  # bounds every context: picks the kernel's register budget
     if splits == 1:
         _lib.call("ts_decode_split", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
                   block_tables.data_ptr(), context_lens.data_ptr(), out.data_ptr(),
-                  None, None, None, b, hq, hkv, d, block_size, *strides, 1, head_tile,
+                  None, None, None, b, hq, hkv, d, block_size, *strides, width, 1, head_tile,
                   scale, dt, stream)  # fmt: skip
         return out
     m = torch.empty((b, hq, splits), dtype=torch.float32, device=q.device)
@@ -159,7 +160,7 @@ def _launch(
     _lib.call("ts_decode_split", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
               block_tables.data_ptr(), context_lens.data_ptr(), out.data_ptr(),
               m.data_ptr(), l.data_ptr(), acc.data_ptr(), b, hq, hkv, d, block_size,
-              *strides, splits, head_tile, scale, dt, stream)  # fmt: skip
+              *strides, width, splits, head_tile, scale, dt, stream)  # fmt: skip
     _lib.call("ts_decode_combine", m.data_ptr(), l.data_ptr(), acc.data_ptr(), out.data_ptr(),
               b, hq, d, out.stride(0), out.stride(1), splits, dt, stream)  # fmt: skip
     return out
