@@ -30,8 +30,10 @@ from tinyserve_amd import _lib
 NO_SPECIALIZE = ["stride_bt", "num_splits"]
 DECODE_TILE = (1, 1)
 
-# Split-K policy (the reference's :488-510, retuned for MI355X). The kernel runs one wave
-# per SIMD (it needs more than 256 VGPRs), and HBM wants about four waves per CU in
+# Split-K policy (the reference's :488-510, retuned for MI355X). On one-round launches of
+# long walks the kernel runs one wave per SIMD (its heavy register budget needs more than
+# 256 VGPRs; launches of several rounds, or whose waves walk under 512 tokens, run a
+# light budget at two per SIMD), and HBM wants about four waves per CU in
 # flight. The library already splits each (sequence, head tile, split) over a workgroup
 # of up to 4 waves that merge in LDS (no HBM partials, no second launch), so a launch of
 # 256 workgroups (one per CU) fills the chip. Splits that write HBM partials are only
@@ -44,7 +46,7 @@ MAX_SPLITS = 16
 
 # Split counts up to this run as one launch: the kernel gives each (sequence, head tile) a
 # workgroup of up to 4 waves over contiguous block ranges, merged in LDS, so there are no
-# fp32 partials in HBM and no combine pass (at B=32 x 256 tokens, 4 splits: 11.9 us
+# fp32 partials in HBM and no combine pass (at B=32 x 256 tokens, 4 splits: 10.8 us
 # against 21.5 us for partials + combine). More splits write partials and combine them.
 IN_GROUP_SPLITS = 4
 
