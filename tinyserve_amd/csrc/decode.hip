@@ -156,21 +156,22 @@ __device__ __forceinline__ void merge_token_lanes(TokenState<T, D, HT, LB>& st) 
   if constexpr (L <= 32) merge_lanes<32>(st);
 }
 
-constexpr int kMaxWavesPerGroup = 4;
+constexpr int kMaxWavesPerGroup = 4;  // heavy budget, and length pairs
+constexpr int kMaxWavesLight = 8;     // light budget (two waves per SIMD)
 
 // The W waves of a decode workgroup each hold a merged state (in their first LPT lanes,
 // lane c holding elements (i * LPT + c) * VEC + j). They park it in LDS, then thread t
 // of the group produces output element t (of HT * D) by the two-partial rule over the W
 // states, and writes it either as the final output (one split) or as the split's fp32
 // partial for the combine pass.
-template <typename T, int D, int HT, typename State, typename Args>
+template <typename T, int D, int HT, int MAXW, typename State, typename Args>
 __device__ __forceinline__ void merge_group_waves(const Args& a, const State& st, int wave,
                                                   int c, int seq, int h0, int split,
                                                   int64_t orow) {
   using S = typename State::S;
   constexpr int NV = S::kNV, VEC = S::kVec, LPT = S::kLPT;
-  __shared__ float sm[kMaxWavesPerGroup][HT], sl[kMaxWavesPerGroup][HT];
-  __shared__ float sacc[kMaxWavesPerGroup][HT][D];
+  __shared__ float sm[MAXW][HT], sl[MAXW][HT];
+  __shared__ float sacc[MAXW][HT][D];
   if (c >= 0) {
 #pragma unroll
     for (int g = 0; g < HT; ++g) {
@@ -242,7 +243,7 @@ __device__ __forceinline__ void park_state(PairSlots<T, D, HT>& ps, const State&
 }
 
 template <typename T, int D, int HT, bool PREFILL, int BUDGET>
-__global__ __launch_bounds__(PREFILL ? kWave : kWave * kMaxWavesPerGroup)
+__global__ __launch_bounds__(PREFILL ? kWave : kWave * (BUDGET == kLight ? kMaxWavesLight : kMaxWavesPerGroup))
 __attribute__((amdgpu_waves_per_eu(BudgetOf<BUDGET>::kWavesPerEU)))
 void paged_attend_kernel(const AttendArgs a) {
   constexpr int LB = BudgetOf<BUDGET>::kLaneBytes;
@@ -480,7 +481,8 @@ void paged_attend_kernel(const AttendArgs a) {
       return;
     }
     if (a.wpg > 1) {
-      merge_group_waves<T, D, HT>(a, st, wave, tl == 0 ? c : -1, seq, h0, split, orow);
+      merge_group_waves<T, D, HT, BUDGET == kLight ? kMaxWavesLight : kMaxWavesPerGroup>(
+          a, st, wave, tl == 0 ? c : -1, seq, h0, split, orow);
       return;
     }
   }
@@ -619,13 +621,16 @@ static int dispatch_d(const AttendArgs& a, int D, int ht, dim3 grid, bool light,
   return TS_EUNSUPPORTED;
 }
 
+// Launches of two or more rounds of one-wave-per-SIMD waves, or whose waves walk few
+// tokens, take the light budget (head tiles of up to two query heads: four heads' state
+// would spill).
+static bool light_budget(int64_t waves, int ht, bool short_walks) {
+  return ht <= 2 && (short_walks || waves >= 8 * static_cast<int64_t>(compute_units()));
+}
+
 template <bool PREFILL>
 static int dispatch_attend(const AttendArgs& a, int dtype, int D, int ht, dim3 grid,
-                           bool short_walks, hipStream_t stream) {
-  // Launches of two or more rounds of one-wave-per-SIMD waves, or whose waves walk few
-  // tokens, take the light budget (head tiles of up to two query heads).
-  const int64_t waves = static_cast<int64_t>(grid.x) * grid.y * grid.z * a.wpg;
-  const bool light = short_walks || waves >= 8 * static_cast<int64_t>(compute_units());
+                           bool light, hipStream_t stream) {
   switch (dtype) {
     case TS_F32: return dispatch_d<float, PREFILL>(a, D, ht, grid, light, stream);
     case TS_F16: return dispatch_d<f16, PREFILL>(a, D, ht, grid, light, stream);
@@ -657,7 +662,8 @@ int prefill_rows_generic(const void* q, const void* k, const void* v, void* out,
                Hq, group, lbs, 1, 1, max_q_len, 0, 0, q_st, q_sh, o_st, o_sh, k_ss, k_sh, bt_s,
                scale * kLog2e};
   dim3 grid(static_cast<unsigned>(R) * max_q_len, Hq / ht, 1);
-  return dispatch_attend<true>(a, dtype, D, ht, grid, false, stream);
+  const int64_t waves = static_cast<int64_t>(grid.x) * grid.y;
+  return dispatch_attend<true>(a, dtype, D, ht, grid, light_budget(waves, ht, false), stream);
 }
 
 template <typename T>
@@ -705,20 +711,25 @@ extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v
   // sequence); one of mixed lengths no longer waits on its longest sequences.
   int by_length = B <= kWave && B >= 2 && splits == 1 && wpg == 2 ? 1 : 0;
   if (by_length) wpg = kMaxWavesPerGroup;
-  AttendArgs a{q, k_cache, v_cache, block_tables, context_lens, out, m, l, acc, nullptr,
-               nullptr, Hq, group, ilog2(block_size), splits, wpg, 0, by_length, B, q_stride_b,
-               q_stride_h, o_stride_b, o_stride_h, k_stride_slot, k_stride_head, bt_stride,
-               scale * kLog2e};
-  dim3 grid(Hq / ht, by_length ? (B + 1) / 2 : B, splits);
   // The table width bounds the tokens a wave walks; waves of at most 256 tokens spend
   // much of their life in start-up and merge, which the light budget's second wave per
   // SIMD hides (measured: +6% to +43% up to 256 tokens a wave; -15% to +4% at 512;
   // -10% from 1024).
   const int64_t walk = static_cast<int64_t>(max_blocks) * block_size * (by_length ? 2 : 1) /
                        (static_cast<int64_t>(splits) * wpg);
-  const bool short_walks = max_blocks > 0 && walk < 512;
-  return dispatch_attend<false>(a, dtype, D, ht, grid, short_walks,
-                                static_cast<hipStream_t>(stream));
+  const int64_t grid_waves =
+      static_cast<int64_t>(Hq / ht) * (by_length ? (B + 1) / 2 : B) * splits * wpg;
+  const bool light = light_budget(grid_waves, ht, max_blocks > 0 && walk < 512);
+  // With two waves per SIMD the chip holds twice the waves: up to 8 per workgroup, so
+  // that each walks fewer tokens (fewer dependent rounds of loads per wave).
+  if (light && !by_length)
+    while (wpg < kMaxWavesLight && waves * wpg * 2 <= 2 * want) wpg *= 2;
+  AttendArgs a{q, k_cache, v_cache, block_tables, context_lens, out, m, l, acc, nullptr,
+               nullptr, Hq, group, ilog2(block_size), splits, wpg, 0, by_length, B, q_stride_b,
+               q_stride_h, o_stride_b, o_stride_h, k_stride_slot, k_stride_head, bt_stride,
+               scale * kLog2e};
+  dim3 grid(Hq / ht, by_length ? (B + 1) / 2 : B, splits);
+  return dispatch_attend<false>(a, dtype, D, ht, grid, light, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int ts_decode_combine(const float* m, const float* l, const float* acc, void* out,
