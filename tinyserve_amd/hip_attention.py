@@ -35,8 +35,9 @@ DECODE_TILE = (1, 1)
 # 256 VGPRs; launches of several rounds, or whose waves walk under 512 tokens, run a
 # light budget at two per SIMD), and HBM wants about four waves per CU in
 # flight. The library already splits each (sequence, head tile, split) over a workgroup
-# of up to 4 waves that merge in LDS (no HBM partials, no second launch), so a launch of
-# 256 workgroups (one per CU) fills the chip. Splits that write HBM partials are only
+# of up to 4 waves (8 under the light budget) that merge in LDS (no HBM partials, no
+# second launch), so a launch of 256 workgroups (one per CU) fills the chip. Splits that
+# write HBM partials are only
 # added below that: the launch aims at TARGET_PROGRAMS workgroups and stops splitting
 # once the batch alone gives NO_SPLIT_PROGRAMS. The reference's T4 values were 1024 and
 # 256 (T4_* below).
@@ -45,9 +46,10 @@ NO_SPLIT_PROGRAMS = 256
 MAX_SPLITS = 16
 
 # Split counts up to this run as one launch: the kernel gives each (sequence, head tile) a
-# workgroup of up to 4 waves over contiguous block ranges, merged in LDS, so there are no
-# fp32 partials in HBM and no combine pass (at B=32 x 256 tokens, 4 splits: 10.8 us
-# against 21.5 us for partials + combine). More splits write partials and combine them.
+# workgroup of up to 4 or 8 waves over contiguous block ranges, merged in LDS, so there
+# are no fp32 partials in HBM and no combine pass (at B=32 x 256 tokens, 4 splits: 10.0
+# us against 21.5 us for partials + combine). More splits write partials and combine
+# them.
 IN_GROUP_SPLITS = 4
 
 # Reference constants, kept for ``num_splits_for(..., target=..., no_split=...)`` callers
