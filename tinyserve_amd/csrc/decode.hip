@@ -14,9 +14,9 @@
 // iteration's math so that three iterations are always in flight).
 //
 // Waves per workgroup. A decode launch gives each (sequence, head tile, split) a
-// workgroup of W = 1, 2, 4 (or 8, light budget) waves; wave w takes the w-th of W contiguous block ranges of
-// the split's range, and the W partial states are merged through LDS before anything is
-// written. This is split-K without HBM partials or a second launch: the library picks W
+// workgroup of W = 1, 2, 4 (or, under the light budget below, 8) waves; wave w takes the
+// w-th of W contiguous block ranges of the split's range, and the W partial states are
+// merged through LDS before anything is written. This is split-K without HBM partials or a second launch: the library picks W
 // so that the grid holds about four waves per CU (the kernel's heavy register budget
 // needs more than 256 VGPRs, so a SIMD runs one wave of it, and a CU wants four in
 // flight to cover HBM latency). Launches of two or more rounds of such waves (many
