@@ -295,14 +295,16 @@ def test_paired_sequences_of_2_to_the_25_tokens() -> None:
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("batch,splits", [(64, 1), (45, 1), (32, 4), (4, 1), (8, 8)])
-def test_both_register_budgets(batch: int, splits: int, dtype: torch.dtype) -> None:
-    # The table width bounds the tokens a wave walks; up to 512 of them the kernel runs
-    # its light budget (two waves per SIMD), else the heavy one. The same sequences
-    # through their own narrow table and through one widened to 2000 blocks give the
-    # reference either way: length pairs (64, 45), in-workgroup splits (32 x 4), a
-    # small batch, and HBM splits with the combine (8 x 8).
+@pytest.mark.parametrize("heads", [(16, 8), (32, 8)])
+def test_both_register_budgets(batch: int, splits: int, heads: tuple[int, int], dtype: torch.dtype) -> None:
+    # The table width bounds the tokens a wave walks; under 512 of them the kernel runs
+    # its light budget (two waves per SIMD, up to 8 a workgroup; 16 bytes a lane for tiles
+    # of four query heads), else the heavy one. The same sequences through their own
+    # narrow table and through one widened to 2000 blocks give the reference either way:
+    # length pairs (64, 45), in-workgroup splits (32 x 4), a small batch, and HBM splits
+    # with the combine (8 x 8), at GQA groups of 2 and 4.
     lens = [1 + (389 * i) % 300 for i in range(batch)]
-    c = decode_case(lens, dtype=dtype, seed=batch)
+    c = decode_case(lens, num_q_heads=heads[0], num_kv_heads=heads[1], dtype=dtype, seed=batch)
     want = oracle32(c)
     g = on_gpu(c)
     for w in (g.block_tables.shape[1], 2000):

@@ -45,7 +45,8 @@ namespace ts {
 // waves all run in one round, where each wave must keep much in flight. kLight: 32 bytes
 // per lane, three in flight, two waves per SIMD -- for launches of several rounds, where
 // the second wave per SIMD hides each wave's start-up chain (lengths, block table, first
-// loads) and merge.
+// loads) and merge. (Tiles of four query heads stream 16 bytes per lane under it, or
+// their state would spill.)
 enum Budget { kHeavy = 0, kLight = 1 };
 template <int B>
 struct BudgetOf {
@@ -246,7 +247,8 @@ template <typename T, int D, int HT, bool PREFILL, int BUDGET>
 __global__ __launch_bounds__(PREFILL ? kWave : kWave * (BUDGET == kLight ? kMaxWavesLight : kMaxWavesPerGroup))
 __attribute__((amdgpu_waves_per_eu(BudgetOf<BUDGET>::kWavesPerEU)))
 void paged_attend_kernel(const AttendArgs a) {
-  constexpr int LB = BudgetOf<BUDGET>::kLaneBytes;
+  // Under the light budget four query heads' state fits only at 16 bytes per lane.
+  constexpr int LB = BUDGET == kLight && HT == 4 ? 16 : BudgetOf<BUDGET>::kLaneBytes;
   using S = RowShape<T, D, LB>;
   constexpr int LPT = S::kLPT, NV = S::kNV, VEC = S::kVec, TPW = S::kTPW, E = S::kE;
   constexpr int NBUF = BudgetOf<BUDGET>::kNBuf;
@@ -586,8 +588,7 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ m
 
 template <typename T, int D, int HT, bool PREFILL>
 static int launch_attend(const AttendArgs& a, dim3 grid, bool light, hipStream_t stream) {
-  // Four query heads' state does not fit the light budget without spilling.
-  if constexpr (HT <= 2) {
+  {
     if (light) {
       hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, PREFILL, kLight>), grid,
                          dim3(kWave * a.wpg), 0, stream, a);
@@ -622,10 +623,9 @@ static int dispatch_d(const AttendArgs& a, int D, int ht, dim3 grid, bool light,
 }
 
 // Launches of two or more rounds of one-wave-per-SIMD waves, or whose waves walk few
-// tokens, take the light budget (head tiles of up to two query heads: four heads' state
-// would spill).
-static bool light_budget(int64_t waves, int ht, bool short_walks) {
-  return ht <= 2 && (short_walks || waves >= 8 * static_cast<int64_t>(compute_units()));
+// tokens, take the light budget.
+static bool light_budget(int64_t waves, bool short_walks) {
+  return short_walks || waves >= 8 * static_cast<int64_t>(compute_units());
 }
 
 template <bool PREFILL>
@@ -663,7 +663,7 @@ int prefill_rows_generic(const void* q, const void* k, const void* v, void* out,
                scale * kLog2e};
   dim3 grid(static_cast<unsigned>(R) * max_q_len, Hq / ht, 1);
   const int64_t waves = static_cast<int64_t>(grid.x) * grid.y;
-  return dispatch_attend<true>(a, dtype, D, ht, grid, light_budget(waves, ht, false), stream);
+  return dispatch_attend<true>(a, dtype, D, ht, grid, light_budget(waves, false), stream);
 }
 
 template <typename T>
@@ -719,7 +719,7 @@ extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v
                        (static_cast<int64_t>(splits) * wpg);
   const int64_t grid_waves =
       static_cast<int64_t>(Hq / ht) * (by_length ? (B + 1) / 2 : B) * splits * wpg;
-  const bool light = light_budget(grid_waves, ht, max_blocks > 0 && walk < 512);
+  const bool light = light_budget(grid_waves, max_blocks > 0 && walk < 512);
   // With two waves per SIMD the chip holds twice the waves: up to 8 per workgroup, so
   // that each walks fewer tokens (fewer dependent rounds of loads per wave).
   if (light && !by_length)
