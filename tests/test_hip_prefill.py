@@ -178,14 +178,16 @@ def test_every_gather_path_on_every_workgroup_shape(block_size: int, shape: tupl
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_length_ranked_sequence_groups(dtype: torch.dtype) -> None:
-    # Batches of 8-16 prompts, of short ones (up to 64), or of 32-64 with equal new-token
-    # counts are dispatched in groups of sequences ranked by context length: 64 short
-    # prompts with ties, 12 mixed ones with prefix hits, 9 whose longest is not first,
-    # and 33 chunks of 600 new tokens after prefixes of different lengths.
+    # Batches of 8-16 prompts, of short ones (up to 64), of 32-64 with equal new-token
+    # counts, or of 17-64 mixed ones are dispatched in groups of sequences ranked by
+    # context length: 64 short prompts with ties, 12 mixed ones with prefix hits, 9 whose
+    # longest is not first, 33 chunks of 600 new tokens after prefixes of different
+    # lengths, and 21 mixed prompts in pairs (an odd count: the last pair is one).
     for specs in ([(0, 1 + (53 * i) % 200) for i in range(64)],
                   [((37 * i) % 300, 1 + (211 * i) % 700) for i in range(12)],
                   [(0, 40)] * 4 + [(5, 900)] + [(0, 40)] * 4,
-                  [((37 * i) % 500, 600) for i in range(33)]):  # fmt: skip
+                  [((37 * i) % 500, 600) for i in range(33)],
+                  [((29 * i) % 90, 300 + (397 * i) % 1100) for i in range(21)]):  # fmt: skip
         c = prefill_case(specs, 16, 8, 128, 16, dtype, seed=len(specs), gap=1)
         out = torch.full_like(c.q, 7.0).to(DEVICE)
         run(c, out=out)

@@ -642,15 +642,19 @@ static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows,
   a.n_kvh = Hkv;
   // Length-ranked groups of 4096 / (mean new tokens) sequences (1 to 8, at most R: a
   // group's K/V about fits one XCD's L2), for 8-16 sequences, short prompts (mean up to
-  // 512 new tokens), or 32 or more prompts of one length, up to 64 sequences. Measured
-  // at Qwen3 shapes: +43% on 8 mixed prompts, +27% on 64 x 256, +5% on 16 x 512, +4-6% on
-  // 48-64 x 1024, +2% on 32 x 2048; on 32 mixed prompts (-3%) and a few long ones (-2.6%
-  // at 4 x 2048; -7 to -12% for 4 equal ones) the plain order is kept.
+  // 512 new tokens), or 32 or more prompts of one length, up to 64 sequences; pairs for
+  // 17-64 prompts of mixed lengths above that mean. Measured at Qwen3 shapes: +43% on 8
+  // mixed prompts, +27% on 64 x 256, +5% on 16 x 512, +4-6% on 48-64 x 1024, +2% on
+  // 32 x 2048, +5.6% on average (-0.4% to +24%) over 16 batches of 24-64 mixed prompts;
+  // for a few long prompts (-2.6% at 4 x 2048; -7 to -12% for 4 equal ones) the plain
+  // order is kept.
   a.seq_group = 0;
   if (a.R > 1 && a.R <= kWave && n_rows > 0) {
     const int64_t mean = (n_rows + a.R - 1) / a.R;
     const bool uniform = n_rows == static_cast<int64_t>(a.R) * max_q_len;
-    if ((a.R >= 8 && a.R <= 16) || mean <= 512 || (uniform && a.R >= 32)) {
+    if (a.R > 16 && !uniform && mean > 512) {
+      a.seq_group = 2;
+    } else if ((a.R >= 8 && a.R <= 16) || mean <= 512 || (uniform && a.R >= 32)) {
       const int g = static_cast<int>(std::min<int64_t>(8, std::max<int64_t>(1, 4096 / std::max<int64_t>(mean, 1))));
       a.seq_group = g < a.R ? g : a.R;
     }
