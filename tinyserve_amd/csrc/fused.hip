@@ -61,13 +61,22 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const T* __restrict_
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const T* xr = x + row * xs;
-  Chunk<T, VEC, ALIGNED> xv[CPL];
-  float ss = 0.f;
+  // The row and the weight are loaded together: the weight's round trip then overlaps
+  // the row's instead of following the reduction.
+  Chunk<T, VEC, ALIGNED> xv[CPL], wv[CPL];
 #pragma unroll
   for (int k = 0; k < CPL; ++k) {
     const int i = (k * 64 + lane) * VEC;
     if (i < N) {
       xv[k].load(xr + i);
+      wv[k].load(w + i);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < CPL; ++k) {
+    const int i = (k * 64 + lane) * VEC;
+    if (i < N) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         const float f = to_f32(xv[k].v[e]);
@@ -82,10 +91,9 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const T* __restrict_
   for (int k = 0; k < CPL; ++k) {
     const int i = (k * 64 + lane) * VEC;
     if (i < N) {
-      Chunk<T, VEC, ALIGNED> wv, y;
-      wv.load(w + i);
+      Chunk<T, VEC, ALIGNED> y;
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) y.v[e] = norm_scale(xv[k].v[e], r, wv.v[e]);
+      for (int e = 0; e < VEC; ++e) y.v[e] = norm_scale(xv[k].v[e], r, wv[k].v[e]);
       y.store(orow + i);
     }
   }
