@@ -221,6 +221,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(const QkArgs a)
   xb.load(src + HALF + off);
   wa.load(wp + off);
   wb.load(wp + HALF + off);
+  // The angles and the key's slot are loaded with the head, not after the reduction.
+  float c[W], s[W];
+#pragma unroll
+  for (int e = 0; e < W; ++e) {
+    c[e] = a.cos[t * a.cs_st + off + e];
+    s[e] = a.sin[t * a.cs_st + off + e];
+  }
+  const int64_t slot = is_q ? 0 : a.slots[t];
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < W; ++e) {
@@ -230,12 +238,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(const QkArgs a)
   }
   ss = group_sum<LPH>(ss);
   const float r = 1.0f / sqrtf(ss / static_cast<float>(D) + a.eps);
-  float c[W], s[W];
-#pragma unroll
-  for (int e = 0; e < W; ++e) {
-    c[e] = a.cos[t * a.cs_st + off + e];
-    s[e] = a.sin[t * a.cs_st + off + e];
-  }
   Chunk<T, W, ALIGNED> ya, yb;
 #pragma unroll
   for (int e = 0; e < W; ++e) {
@@ -251,7 +253,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(const QkArgs a)
     ya.store(dst + off);
     yb.store(dst + HALF + off);
   } else {
-    TC* dst = static_cast<TC*>(a.kc) + a.slots[t] * a.c_ss + hh * a.c_sh;
+    TC* dst = static_cast<TC*>(a.kc) + slot * a.c_ss + hh * a.c_sh;
     Chunk<TC, W, ALIGNED> za, zb;
 #pragma unroll
     for (int e = 0; e < W; ++e) {
