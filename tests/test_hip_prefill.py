@@ -182,12 +182,15 @@ def test_length_ranked_sequence_groups(dtype: torch.dtype) -> None:
     # counts, or of 17-64 mixed ones are dispatched in groups of sequences ranked by
     # context length: 64 short prompts with ties, 12 mixed ones with prefix hits, 9 whose
     # longest is not first, 33 chunks of 600 new tokens after prefixes of different
-    # lengths, and 21 mixed prompts in pairs (an odd count: the last pair is one).
+    # lengths, 21 mixed prompts in pairs (an odd count: the last pair is one), and two
+    # batches already in rank order (no ranking loop), one with ties.
     for specs in ([(0, 1 + (53 * i) % 200) for i in range(64)],
                   [((37 * i) % 300, 1 + (211 * i) % 700) for i in range(12)],
                   [(0, 40)] * 4 + [(5, 900)] + [(0, 40)] * 4,
                   [((37 * i) % 500, 600) for i in range(33)],
-                  [((29 * i) % 90, 300 + (397 * i) % 1100) for i in range(21)]):  # fmt: skip
+                  [((29 * i) % 90, 300 + (397 * i) % 1100) for i in range(21)],
+                  [(0, 900 - 60 * i) for i in range(12)],
+                  [(0, 500)] * 3 + [(0, 300)] * 6):  # fmt: skip
         c = prefill_case(specs, 16, 8, 128, 16, dtype, seed=len(specs), gap=1)
         out = torch.full_like(c.q, 7.0).to(DEVICE)
         run(c, out=out)

@@ -233,10 +233,21 @@ prefill_mfma_kernel(const PrefillArgs a) {
     if (want >= a.R) return;
     const int ln = threadIdx.x & (kWave - 1);
     const int mine = ln < a.R ? a.ctx_lens[ln] : -1;
-    int rank = 0;
-    for (int j = 0; j < a.R; ++j) {
-      const int other = __builtin_amdgcn_readlane(mine, j);
-      rank += (other > mine) | ((other == mine) & (j < ln));
+    // Already in rank order (non-increasing lengths): no ranking loop.
+    const int next = __shfl_down(mine, 1);
+    int rank = ln;
+    if (!__all(ln + 1 >= a.R || mine >= next)) {
+      rank = 0;
+      if (__all(mine < (1 << 25))) {
+        // Unique keys (length, then lower index first): rank = keys above this one.
+        const int key = ln < a.R ? mine * kWave + (kWave - 1 - ln) : -1;
+        for (int j = 0; j < a.R; ++j) rank += __builtin_amdgcn_readlane(key, j) > key;
+      } else {
+        for (int j = 0; j < a.R; ++j) {
+          const int other = __builtin_amdgcn_readlane(mine, j);
+          rank += (other > mine) | ((other == mine) & (j < ln));
+        }
+      }
     }
     r = __builtin_ctzll(__ballot(ln < a.R && rank == want));
   } else {
