@@ -177,6 +177,21 @@ def test_every_gather_path_on_every_workgroup_shape(block_size: int, shape: tupl
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("heads", [(16, 8, 128), (32, 8, 128), (8, 2, 64)])
+def test_key_split_workgroups(dtype: torch.dtype, heads: tuple[int, int, int]) -> None:
+    # One or two prompts run workgroups whose waves split the key tiles in two halves
+    # and merge at the end: one key tile (the upper half empty), odd and even tile
+    # counts, a query block whose keys end before the upper half, prefix hits (the
+    # halves split the cached keys too), and block sizes below the scalar-id gather's
+    # (the unsplit 4-wave kernel).
+    for specs, bs in (([(0, 1)], 16), ([(0, 64)], 16), ([(0, 65)], 16), ([(0, 200)], 16),
+                      ([(0, 1000)], 32), ([(300, 37)], 16), ([(100, 2048)], 16),
+                      ([(0, 700), (9, 1300)], 64), ([(0, 500)], 2), ([(33, 400)], 1)):  # fmt: skip
+        c = prefill_case(specs, *heads, bs, dtype, seed=bs + len(specs))
+        check(c, run(c))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_length_ranked_sequence_groups(dtype: torch.dtype) -> None:
     # Batches of 8-16 prompts, of short ones (up to 64), of 32-64 with equal new-token
     # counts, or of 17-64 mixed ones are dispatched in groups of sequences ranked by

@@ -31,11 +31,15 @@
 //
 // Three shapes: 8 waves with a 3-stage ring of 64-key tiles (one workgroup per CU, 98 KB
 // of LDS, two waves per SIMD) for large launches and prefix-hit chunks; for launches with
-// too few query tiles to fill the chip that way, 4 waves with a 2-stage ring (66 KB: two
-// workgroups per CU, half the queries per workgroup); and for mid-size launches, 4 waves
-// over 32-key tiles (a 2-stage ring of 34 KB, 157 VGPRs: three workgroups, so three
-// waves, per SIMD), whose extra wave per SIMD and finer key tiles outweigh the doubled
-// barriers there.
+// too few query tiles to fill the chip that way (one or two prompts), 8 waves over the
+// queries of the 4-wave shape (64 x 2 heads) with the keys split in two: waves w and
+// w + 4 walk the lower and upper half of the key tiles (a 2-stage ring holding one tile
+// of each half, 128 KB) and merge their softmax states through LDS at the end, which
+// halves the longest workgroup's walk and puts two waves on each SIMD; and for mid-size
+// launches, 4 waves over 32-key tiles (a 2-stage ring of 34 KB, 157 VGPRs: three
+// workgroups, so three waves, per SIMD), whose extra wave per SIMD and finer key tiles
+// outweigh the doubled barriers there. (Block sizes under 4 slots, 8 at D=64, run 4
+// waves without the split: the halves' block ids come from the scalar-id gather.)
 //
 // MFMA formulation (v_mfma_f32_32x32x16_{f16,bf16}). Scores are computed transposed,
 // S^T[key, query] = K . Q^T, with K as the A operand (one 16-byte LDS read per lane) and
@@ -184,11 +188,16 @@ __device__ __forceinline__ void ring_barrier() {
 }
 
 template <typename T, int D, int HG, int QB, int kWaves, int kStages, int kBN, int kOcc,
-          bool kScalarIds>
+          bool kScalarIds, bool kSplitK>
 __global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(kOcc, kOcc))) void
 prefill_mfma_kernel(const PrefillArgs a) {
   using V8 = typename Mfma<T>::V8;
-  using Sh = TileShape<D, kWaves, kBN>;
+  // Key split: waves w and w + kWaves / 2 take the same queries and heads; the first
+  // walks the lower half of the workgroup's key tiles, the second the upper half, and
+  // the two softmax states are merged through LDS at the end. kGW waves share a tile.
+  constexpr int kGW = kSplitK ? kWaves / 2 : kWaves;
+  static_assert(!kSplitK || (kScalarIds && kStages == 2), "key split: scalar ids, 2 stages");
+  using Sh = TileShape<D, kGW, kBN>;
   constexpr int NH = kBN / 32;  // 32-key halves of S^T (one MFMA accumulator each)
   constexpr int NC = kBN / 16;  // 16-key chunks of P^T (one PV B operand each)
   static_assert(kStages == 2 || kStages == 3, "ring of 2 or 3 stages");
@@ -204,13 +213,16 @@ prefill_mfma_kernel(const PrefillArgs a) {
   // and P.V takes two MFMAs. fp16's 11 bits meet the tolerance with one.
   constexpr bool kSplitP = std::is_same_v<T, bf16>;
 
-  __shared__ __attribute__((aligned(16))) T k_ring[kStages * TILE];
-  __shared__ __attribute__((aligned(16))) T v_ring[kStages * TILE];
+  constexpr int kStageStride = (kSplitK ? 2 : 1) * TILE;  // one tile per key half
+  __shared__ __attribute__((aligned(16))) T k_ring[kStages * kStageStride];
+  __shared__ __attribute__((aligned(16))) T v_ring[kStages * kStageStride];
   __shared__ int32_t ids_lds[kWin];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kh = kSplitK ? wave / kGW : 0;           // key half
+  const int wl = kSplitK ? wave - kh * kGW : wave;  // wave within its half
   const int col = lane & 31;  // this lane's query within the wave's 32
   const int half = lane >> 5;
 
@@ -262,8 +274,8 @@ prefill_mfma_kernel(const PrefillArgs a) {
   const int q_start = a.q_starts[r];
   const int kvh = hcx / a.hchunks;
   const int hc = hcx - kvh * a.hchunks;
-  const int hg = wave % HG;
-  const int qb = wave / HG;
+  const int hg = wl % HG;
+  const int qb = wl / HG;
   const int head = kvh * a.group + hc * HG + hg;
   const int past = ctx - q_len;  // position of query 0 is past + 0
 
@@ -334,7 +346,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
   uint32_t kunit[IPW], vunit[IPW], rows_bytes[IPW];
 #pragma unroll
   for (int m = 0; m < IPW; ++m) {
-    const int row = (wave * IPW + m) * RPI + dma_row;
+    const int row = (wl * IPW + m) * RPI + dma_row;
     kunit[m] = 16u * static_cast<uint32_t>(dma_unit ^ k_swz<D>(row));
     vunit[m] = 16u * static_cast<uint32_t>(dma_unit ^ v_swz<D>(row));
     rows_bytes[m] = static_cast<uint32_t>(m * RPI + dma_row) * k_ss_bytes;
@@ -346,7 +358,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
       if (wave_block) {
         // One block id and one base for all of the wave's loads; rows past key_last
         // read key_last, which lies in the same block.
-        const int kw = __builtin_amdgcn_readfirstlane(min(n0 + wave * IPW * RPI, key_last));
+        const int kw = __builtin_amdgcn_readfirstlane(min(n0 + wl * IPW * RPI, key_last));
         const int blk = bt_c[kw >> lbs];
         const uint64_t boff = ((static_cast<uint64_t>(static_cast<uint32_t>(blk)) << lbs) +
                                static_cast<uint32_t>(kw & bs_mask)) * k_ss_bytes;
@@ -355,7 +367,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
         const char* vb = reinterpret_cast<const char*>(vbase) + boff;
 #pragma unroll
         for (int m = 0; m < IPW; ++m) {
-          const int row0 = (wave * IPW + m) * RPI;
+          const int row0 = (wl * IPW + m) * RPI;
           const uint32_t voff = min(rows_bytes[m], lim);
           lds_load16_s(kb, voff + kunit[m], (TS_LDS void*)(k_lds + row0 * D));
           lds_load16_s(vb, voff + vunit[m], (TS_LDS void*)(v_lds + row0 * D));
@@ -366,12 +378,12 @@ prefill_mfma_kernel(const PrefillArgs a) {
       int key0[IPW], blk[IPW];
 #pragma unroll
       for (int m = 0; m < IPW; ++m) {
-        key0[m] = __builtin_amdgcn_readfirstlane(min(n0 + (wave * IPW + m) * RPI, key_last));
+        key0[m] = __builtin_amdgcn_readfirstlane(min(n0 + (wl * IPW + m) * RPI, key_last));
         blk[m] = bt_c[key0[m] >> lbs];
       }
 #pragma unroll
       for (int m = 0; m < IPW; ++m) {
-        const int row0 = (wave * IPW + m) * RPI;
+        const int row0 = (wl * IPW + m) * RPI;
         const uint64_t slot0 = (static_cast<uint64_t>(static_cast<uint32_t>(blk[m])) << lbs) +
                                static_cast<uint32_t>(key0[m] & bs_mask);
         const uint64_t boff = slot0 * k_ss_bytes;
@@ -386,7 +398,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
 #pragma unroll
     for (int m = 0; m < IPW; ++m) {
-      const int row0 = (wave * IPW + m) * RPI;
+      const int row0 = (wl * IPW + m) * RPI;
       const int row = row0 + dma_row;
       const int key = min(n0 + row, key_last);
       const int blk = ids_lds[(key >> lbs) - win_blk0];
@@ -579,17 +591,37 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
     if (n0 < wave_key_end) attend(k_cur, v_cur, n0);
   };
-  T* const k0 = k_ring;
-  T* const v0 = v_ring;
-  T* const k1 = k_ring + TILE;
-  T* const v1 = v_ring + TILE;
-  T* const k2 = k_ring + (kStages - 1) * TILE;  // == k1 with two stages (never used)
-  T* const v2 = v_ring + (kStages - 1) * TILE;
+  // Stage s of this wave's key half: one tile, at (s * halves + kh) tiles.
+  T* const k0 = k_ring + kh * TILE;
+  T* const v0 = v_ring + kh * TILE;
+  T* const k1 = k0 + kStageStride;
+  T* const v1 = v0 + kStageStride;
+  T* const k2 = k0 + (kStages - 1) * kStageStride;  // == k1 with two stages (never used)
+  T* const v2 = v0 + (kStages - 1) * kStageStride;
 
   if constexpr (!kScalarIds) {
     fill_window(0);
     __syncthreads();
   }
+  if constexpr (kSplitK) {
+    // The lower half takes tiles 0 .. n_lo - 1, the upper half the rest; both step n_lo
+    // times (the same barriers), the upper half's last step possibly with no tile.
+    const int ntiles = (key_end + kBN - 1) / kBN;
+    const int n_lo = (ntiles + 1) / 2;
+    const int base = kh * n_lo * kBN;
+    const int half_end = kh ? key_end : min(n_lo * kBN, key_end);
+    auto sstep = [&](const T* k_cur, const T* v_cur, T* k_nx, T* v_nx, int n0) {
+      ring_barrier<0>();
+      if (n0 + kBN < half_end) gather(k_nx, v_nx, n0 + kBN);
+      if (n0 < half_end && n0 < wave_key_end) attend(k_cur, v_cur, n0);
+    };
+    if (base < half_end) gather(k0, v0, base);
+    for (int i = 0; i < n_lo; i += 2) {
+      sstep(k0, v0, k1, v1, base + i * kBN);
+      if (i + 1 >= n_lo) break;
+      sstep(k1, v1, k0, v0, base + (i + 1) * kBN);
+    }
+  } else {
   gather(k0, v0, 0);
   if constexpr (kStages == 3) {
     if (kBN < key_end) gather(k1, v1, kBN);
@@ -607,8 +639,41 @@ prefill_mfma_kernel(const PrefillArgs a) {
       step(k1, v1, k0, v0, n0 + kBN);
     }
   }
+  }
   // No load may still be writing this workgroup's LDS when its waves end.
   __builtin_amdgcn_s_waitcnt(0x0070);
+
+  if constexpr (kSplitK) {
+    // Merge the upper half's state into the lower half's, lane by lane (the two waves
+    // have the same layout): m, l and O^T[0] through k_ring, O^T[1..] through v_ring,
+    // lane-fastest so that the accesses are conflict-free. Scores are in base-2 units.
+    __syncthreads();  // every wave is done with the ring
+    float* xk = reinterpret_cast<float*>(k_ring) + wl * (2 + 16) * kWave + lane;
+    float* xv = reinterpret_cast<float*>(v_ring) + wl * (DT - 1) * 16 * kWave + lane;
+    if (kh == 1) {
+      xk[0] = m_run;
+      xk[kWave] = l_run;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xk[(2 + e) * kWave] = oacc[0][e];
+#pragma unroll
+      for (int dt = 1; dt < DT; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xv[((dt - 1) * 16 + e) * kWave] = oacc[dt][e];
+    }
+    __syncthreads();
+    if (kh == 1) return;
+    const float m1 = xk[0];
+    const float mn = fmaxf(m_run, m1);
+    const float a0 = fast_exp2(m_run - mn), a1 = fast_exp2(m1 - mn);
+    l_run = l_run * a0 + xk[kWave] * a1;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[0][e] = oacc[0][e] * a0 + xk[(2 + e) * kWave] * a1;
+#pragma unroll
+    for (int dt = 1; dt < DT; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) oacc[dt][e] = oacc[dt][e] * a0 + xv[((dt - 1) * 16 + e) * kWave] * a1;
+    m_run = mn;
+  }
 
   const float l_tot = halves_sum(l_run);
   if (!q_ok) return;
@@ -627,16 +692,23 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
 }
 
-template <typename T, int D, int HG, int W, int S, int BN, int OCC>
+// SPLIT: the key-split shape (W waves, W / 2 per key half); its caller checks that the
+// block size allows the scalar-id gather.
+template <typename T, int D, int HG, int W, int S, int BN, int OCC, bool SPLIT = false>
 static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream) {
-  constexpr int QB = W / HG;
+  constexpr int QB = (SPLIT ? W / 2 : W) / HG;
   const int seqs = a.seq_group > 0 ? (a.R + a.seq_group - 1) / a.seq_group * a.seq_group : a.R;
   dim3 grid(static_cast<unsigned>(a.n_qtiles) * seqs * Hkv * a.hchunks);
+  if constexpr (SPLIT) {
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, true, true>), grid,
+                       dim3(W * kWave), 0, stream, a);
+    return launch_status();
+  }
   // A load's RPI rows share a cache block when blocks hold at least RPI slots.
   if ((1 << a.lbs) >= TileShape<D, W, BN>::kRPI)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, true>), grid, dim3(W * kWave), 0, stream, a);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, true, false>), grid, dim3(W * kWave), 0, stream, a);
   else
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, false>), grid, dim3(W * kWave), 0, stream, a);
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, false, false>), grid, dim3(W * kWave), 0, stream, a);
   return launch_status();
 }
 
@@ -644,11 +716,12 @@ static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream
 // work; the 4-wave shape halves the work per workgroup and fits two workgroups per CU,
 // which wins when the launch has fewer than two 8-wave workgroups per CU (e.g. one
 // 2048-token prompt: 128 workgroups of 8 waves).
-template <typename T, int D, int W, int S, int BN, int OCC>
+template <typename T, int D, int W, int S, int BN, int OCC, bool SPLIT = false>
 static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows, hipStream_t stream) {
-  const int hg = a.group < W ? a.group : W;
+  constexpr int WQ = SPLIT ? W / 2 : W;  // waves over the queries and heads
+  const int hg = a.group < WQ ? a.group : WQ;
   a.hchunks = a.group / hg;
-  const int bq = 32 * (W / hg);
+  const int bq = 32 * (WQ / hg);
   a.n_qtiles = (max_q_len + bq - 1) / bq;
   a.n_kvh = Hkv;
   // Length-ranked groups of 4096 / (mean new tokens) sequences (1 to 8, at most R: a
@@ -671,11 +744,13 @@ static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows,
     }
   }
   switch (hg) {
-    case 1: return launch_prefill_mfma<T, D, 1, W, S, BN, OCC>(a, Hkv, stream);
-    case 2: return launch_prefill_mfma<T, D, 2, W, S, BN, OCC>(a, Hkv, stream);
-    case 4: return launch_prefill_mfma<T, D, 4, W, S, BN, OCC>(a, Hkv, stream);
+    case 1: return launch_prefill_mfma<T, D, 1, W, S, BN, OCC, SPLIT>(a, Hkv, stream);
+    case 2: return launch_prefill_mfma<T, D, 2, W, S, BN, OCC, SPLIT>(a, Hkv, stream);
+    case 4:
+      if constexpr (WQ >= 4) return launch_prefill_mfma<T, D, 4, W, S, BN, OCC, SPLIT>(a, Hkv, stream);
+      return TS_EUNSUPPORTED;
     case 8:
-      if constexpr (W >= 8) return launch_prefill_mfma<T, D, 8, W, S, BN, OCC>(a, Hkv, stream);
+      if constexpr (WQ >= 8) return launch_prefill_mfma<T, D, 8, W, S, BN, OCC, SPLIT>(a, Hkv, stream);
       return TS_EUNSUPPORTED;
     default: return TS_EUNSUPPORTED;
   }
@@ -709,7 +784,12 @@ template <typename T, int D>
 static int dispatch_hg(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows, hipStream_t stream) {
   switch (prefill_shape(a.R, a.group, Hkv, max_q_len, n_rows)) {
     case PrefillShape::kW4Short: return dispatch_hg_w<T, D, 4, 2, 32, 3>(a, Hkv, max_q_len, n_rows, stream);
-    case PrefillShape::kW4: return dispatch_hg_w<T, D, 4, 2, 64, 2>(a, Hkv, max_q_len, n_rows, stream);
+    case PrefillShape::kW4:
+      // Two key halves per workgroup (8 waves, one workgroup and two waves per SIMD per
+      // CU) where the scalar-id gather applies; else the plain 4-wave shape.
+      if ((1 << a.lbs) >= TileShape<D, 4, 64>::kRPI)
+        return dispatch_hg_w<T, D, 8, 2, 64, 2, true>(a, Hkv, max_q_len, n_rows, stream);
+      return dispatch_hg_w<T, D, 4, 2, 64, 2>(a, Hkv, max_q_len, n_rows, stream);
     default: return dispatch_hg_w<T, D, 8, 3, 64, 2>(a, Hkv, max_q_len, n_rows, stream);
   }
 }
