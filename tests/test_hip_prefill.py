@@ -182,10 +182,12 @@ def test_key_split_workgroups(dtype: torch.dtype, heads: tuple[int, int, int]) -
     # One or two prompts run workgroups whose waves split the key tiles in two halves
     # and merge at the end: one key tile (the upper half empty), odd and even tile
     # counts, a query block whose keys end before the upper half, prefix hits (the
-    # halves split the cached keys too), and block sizes below the scalar-id gather's
-    # (the unsplit 4-wave kernel).
+    # halves split the cached keys too; chunks of at most 64 new tokens in small launches
+    # run this shape as well), and block sizes below the scalar-id gather's (the unsplit
+    # 4-wave kernel).
     for specs, bs in (([(0, 1)], 16), ([(0, 64)], 16), ([(0, 65)], 16), ([(0, 200)], 16),
                       ([(0, 1000)], 32), ([(300, 37)], 16), ([(100, 2048)], 16),
+                      ([(1024, 64)] * 4, 16), ([(8000, 50)], 16),
                       ([(0, 700), (9, 1300)], 64), ([(0, 500)], 2), ([(33, 400)], 1)):  # fmt: skip
         c = prefill_case(specs, *heads, bs, dtype, seed=bs + len(specs))
         check(c, run(c))
