@@ -16,6 +16,18 @@
  *   k_cache, v_cache   [num_slots, Hkv, D]   one layer; (stride_slot, stride_head, 1)
  *   block_tables       [B or R, W] int32     row stride bt_stride
  *   slot of position p = block_tables[row, p / block_size] * block_size + p % block_size
+ *
+ * Device-resident inputs are trusted, as the kernels cannot check them without a host
+ * sync. The caller guarantees what the reference's Python checks before its launches
+ * (check_decode_args, triton_attention.py:361-391; paged_prefill_attention,
+ * triton_prefill.py:177-194):
+ *   - every context length is at least 1, and the table row holds every block it
+ *     covers, each a valid block of the cache;
+ *   - for prefill, 0 <= q_lens[r] <= min(context_lens[r], max_q_len) (a sequence with
+ *     no new rows is skipped), and rows
+ *     q_starts[r] .. q_starts[r] + q_lens[r] - 1 exist in q and out;
+ *   - slots passed to ts_qk_norm_rope_store lie in the cache.
+ * Inputs outside these ranges make the kernels read or write out of bounds.
  */
 #ifndef TINYSERVE_AMD_H
 #define TINYSERVE_AMD_H
