@@ -318,7 +318,7 @@ def main() -> None:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--profile", choices=["prefill_varlen32"], default=None,
+    ap.add_argument("--profile", choices=["prefill_varlen32", "fused_t4096"], default=None,
                     help="only launch one workload 3 times (for a profiler) and print what ran")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run 3 plain device copies of this many MiB (a known-size kernel "
@@ -340,7 +340,18 @@ def main() -> None:
         for _ in range(3):
             paged_prefill_attention(*p.args(), out=out)
         torch.cuda.synchronize()
-        print(json.dumps({"profile": args.profile, "launches": 3, "sequences": len(lens)}), flush=True)
+        print(json.dumps({"profile": args.profile, "launches": 3, "sequences": len(lens),
+                          **calibration_copies(args.copy_mb)}), flush=True)  # fmt: skip
+        return
+    if args.profile == "fused_t4096":  # config 4's two fused kernels, eager, nothing else
+        f = fused_case(device=torch.device("cuda:0"), sentinel=False)
+        for _ in range(3):
+            rms_norm_rows(f.x, f.norm_w, f.eps)
+        for _ in range(3):
+            qk_norm_rope_store(f.q, f.k, f.v, f.q_w, f.k_w, f.cos, f.sin, f.slots, f.k_cache, f.v_cache, f.eps)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": args.profile, "launches": 3, "tokens": f.x.shape[0],
+                          **calibration_copies(args.copy_mb)}), flush=True)  # fmt: skip
         return
     nb = math.ceil(args.ctx / BS)
     splits = args.splits or num_splits_for(args.batch, HKV, nb)
@@ -382,14 +393,21 @@ def main() -> None:
         line["cpu_baseline"] = cpu_baseline(r["case"], splits)
     if not args.no_extra:
         line["extra"] = extra_measurements()
-    if args.copy_mb:
-        src = torch.ones(args.copy_mb << 18, dtype=torch.float32, device="cuda:0")
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        line["copy_calibration_bytes"] = {"read": src.numel() * 4, "write": dst.numel() * 4}
+    line.update(calibration_copies(args.copy_mb))
     print(json.dumps(line), flush=True)
+
+
+def calibration_copies(mb: int) -> dict:
+    """Three plain device copies of ``mb`` MiB (none if 0): a kernel of known traffic
+    that calibrates a profiler's HBM byte counters."""
+    if not mb:
+        return {}
+    src = torch.ones(mb << 18, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"copy_calibration_bytes": {"read": src.numel() * 4, "write": dst.numel() * 4}}
 
 
 if __name__ == "__main__":
