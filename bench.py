@@ -382,7 +382,7 @@ def main() -> None:
                                   else f"split-K {splits} + combine"),
                    "batch": args.batch, "ctx": args.ctx, "splits": splits,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "paged_attend_kernel<f16,128,2,false,heavy>",
+        "roofline": {"bound": "hbm", "kernel": "paged_attend_kernel<f16,128,2,false,light-stream>",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "avg_launch_us": round(r["split_ms"] * 1e3, 2),

@@ -734,24 +734,34 @@ extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v
                        (static_cast<int64_t>(splits) * wpg);
   const int64_t grid_waves =
       static_cast<int64_t>(Hq / ht) * (by_length ? (B + 1) / 2 : B) * splits * wpg;
-  const bool light = light_budget(grid_waves, max_blocks > 0 && walk < 512);
+  // K/V (bounded by the table width) larger than the 256 MiB last-level cache: it is read
+  // once, so it goes through non-temporal loads (caching it only evicts other lines), under
+  // the light budget, in workgroups of up to 8 waves sized for one round of the chip
+  // (8 waves per CU), without length pairs. Measured against the heavy one-round launch:
+  // +13% to +16.5% at 64 x 4096 (189.6 -> 164.9 us, 6.5 TB/s), 32 x 4096, 64 x 2048,
+  // 16 x 8192 and 128 x 4096; -4.8% for 64 mixed lengths in U[1024, 4096], which lose
+  // their pairs. Smaller launches keep cached loads, which let K/V that a previous step
+  // left in the cache be read from there (32 x 256: -13% with non-temporal loads).
+  const int64_t kv_bytes = static_cast<int64_t>(B) * max_blocks * block_size * Hkv * D *
+                           (dtype == TS_F32 ? 4 : 2) * 2;
+  const bool stream_kv = max_blocks > 0 && kv_bytes > (int64_t{256} << 20);
+  if (stream_kv && by_length) {
+    by_length = 0;
+    wpg = 1;
+  }
+  const bool light = stream_kv || light_budget(grid_waves, max_blocks > 0 && walk < 512);
   // With two waves per SIMD the chip holds twice the waves: up to 8 per workgroup, so
   // that each walks fewer tokens (fewer dependent rounds of loads per wave).
-  if (light && !by_length)
+  if (stream_kv) {
+    while (wpg < kMaxWavesLight && waves * wpg < 2 * want) wpg *= 2;
+  } else if (light && !by_length) {
     while (wpg < kMaxWavesLight && waves * wpg * 2 <= 2 * want) wpg *= 2;
+  }
   AttendArgs a{q, k_cache, v_cache, block_tables, context_lens, out, m, l, acc, nullptr,
                nullptr, Hq, group, ilog2(block_size), splits, wpg, 0, by_length, B, q_stride_b,
                q_stride_h, o_stride_b, o_stride_h, k_stride_slot, k_stride_head, bt_stride,
                scale * kLog2e, 0};
-  // Light-budget launches whose K/V (bounded by the table width) exceeds the 256 MiB
-  // last-level cache read it with non-temporal loads: it is read once, and caching it
-  // only evicts other lines (measured +9% to +14%: 256 x 1024, 512 x 512, 64 mixed
-  // sequences in 16 splits). Smaller launches keep cached loads, which let K/V that a
-  // previous step left in the cache be read from there (32 x 256: -13% with such loads).
-  // The heavy budget keeps cached loads at any size (-12% at 64 x 4096 with them).
-  const int64_t kv_bytes = static_cast<int64_t>(B) * max_blocks * block_size * Hkv * D *
-                           (dtype == TS_F32 ? 4 : 2) * 2;
-  a.stream_kv = light && kv_bytes > (int64_t{256} << 20) ? 1 : 0;
+  a.stream_kv = stream_kv ? 1 : 0;
   dim3 grid(Hq / ht, by_length ? (B + 1) / 2 : B, splits);
   return dispatch_attend<false>(a, dtype, D, ht, grid, light, static_cast<hipStream_t>(stream));
 }
