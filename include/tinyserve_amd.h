@@ -73,10 +73,12 @@ const char* ts_strerror(int code);
  * ts_decode_combine finishes the result. m is stored in base-2 units (log2 e * max score).
  *
  * max_blocks: the width of block_tables (entries per row the caller filled, so every
- * context is at most max_blocks * block_size), or 0 if unknown. It only picks the
- * kernel's register budget (short walks per wave run two waves per SIMD); nothing is
- * read by it, and a wrong value costs speed, never correctness. (The reference passes
- * the table to Triton and has no such argument.)
+ * context is at most max_blocks * block_size), or 0 if unknown. It only picks how the
+ * launch runs: the register budget (short walks per wave run two waves per SIMD) and,
+ * when the K/V it bounds exceeds 256 MiB, non-temporal K/V loads with one round of
+ * two-wave-per-SIMD workgroups. Nothing is read by it, and a wrong value costs speed,
+ * never correctness. (The reference passes the table to Triton and has no such
+ * argument.)
  */
 int ts_decode_split(const void* q, const void* k_cache, const void* v_cache,
                     const int32_t* block_tables, const int32_t* context_lens, void* out,
