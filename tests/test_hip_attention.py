@@ -359,3 +359,26 @@ def test_combine_over_many_splits(splits: int, head_dim: int, dtype: torch.dtype
     out = ha._launch(*g.args(), g.scale, g.block_size, splits, 0)
     assert torch.isfinite(out).all()
     assert_matches(out, want, dtype, f"splits={splits} D={head_dim}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_streaming_launches(dtype: torch.dtype, head_dim: int) -> None:
+    # A table wide enough to bound more than 256 MiB of K/V makes the launch stream K/V
+    # with non-temporal loads (light budget, one round of workgroups, no length pairs);
+    # the unused columns are never read. The results match the oracle and the launch
+    # over the tight table, for one split and for HBM splits.
+    lens = [1, 17, 300, 64, 1000, 5, 700, 33] * 4
+    c = decode_case(lens, head_dim=head_dim, dtype=dtype, seed=11)
+    want = oracle32(c)
+    g = on_gpu(c)
+    b, w = g.block_tables.shape
+    wide = torch.full((b, 8192), -1, dtype=torch.int32, device=DEVICE)  # -1: never read
+    wide[:, :w] = g.block_tables
+    for splits in (1, 4):
+        tight = ha.launch_paged_decode_split(*g.args(), g.scale, g.block_size, num_splits=splits)
+        out = ha.launch_paged_decode_split(g.q, g.k_cache, g.v_cache, wide, g.context_lens, g.scale,
+                                           g.block_size, num_splits=splits)  # fmt: skip
+        assert torch.isfinite(out).all(), splits
+        assert_matches(out, want, dtype, f"streaming, {splits} split(s)")
+        torch.testing.assert_close(out, tight, atol=TOL[dtype], rtol=TOL[dtype])
