@@ -33,7 +33,8 @@ DECODE_TILE = (1, 1)
 # Split-K policy (the reference's :488-510, retuned for MI355X). On one-round launches of
 # long walks the kernel runs one wave per SIMD (its heavy register budget needs more than
 # 256 VGPRs; launches of several rounds, or whose waves walk under 512 tokens, run a
-# light budget at two per SIMD), and HBM wants about four waves per CU in
+# light budget at two per SIMD, and so do launches whose K/V exceeds the 256 MiB
+# last-level cache, with non-temporal loads), and HBM wants about four waves per CU in
 # flight. The library already splits each (sequence, head tile, split) over a workgroup
 # of up to 4 waves (8 under the light budget) that merge in LDS (no HBM partials, no
 # second launch), so a launch of 256 workgroups (one per CU) fills the chip. Splits that
