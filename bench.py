@@ -33,7 +33,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 from tinyserve_amd import _lib  # noqa: E402
-from tinyserve_amd.hip_attention import launch_paged_decode_split, num_splits_for  # noqa: E402
+from tinyserve_amd.hip_attention import decode_plan, launch_paged_decode_split, num_splits_for  # noqa: E402
 from tinyserve_amd.hip_fused import qk_norm_rope_store, rms_norm_rows  # noqa: E402
 from tinyserve_amd.hip_prefill import paged_prefill_attention  # noqa: E402
 from tinyserve_amd.workloads import (  # noqa: E402
@@ -154,6 +154,16 @@ def graph_ms(fn, launches: int = 20, replays: int = 10) -> float:
     return a.elapsed_time(b) / (replays * launches)
 
 
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(case, splits: int, budget_s: float = 15.0) -> dict:
     """The oracle (PyTorch reference path restated) on this host, over the same 64 x 4096
     workload, repeated until ``budget_s`` of work (at least once)."""
@@ -172,9 +182,57 @@ def cpu_baseline(case, splits: int, budget_s: float = 15.0) -> dict:
     dt = (time.perf_counter() - t0) / reps
     nbytes = decode_bytes(q.shape[0], int(lens[0]))["step"]
     return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "cpu_model": cpu_model(), "kind": "port",
             "sample": f"oracle.ref.decode_ref (torch CPU) over the full B={q.shape[0]} x ctx="
                       f"{int(lens[0])} fp16 workload, {reps} rep(s), {dt:.2f} s each"}  # fmt: skip
+
+
+def cpu_baselines_other_configs(budget_s: float = 8.0) -> dict:
+    """The oracle on this host for configs 3 (varlen prefill, fp16) and 4 (fused norm /
+    RoPE / KV write, T=4096): bounded samples of the same workloads, scaled by their
+    algorithmic flops or bytes."""
+    from oracle import ref
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    res: dict = {"cores": torch.get_num_threads(), "cpu_model": cpu_model(), "kind": "port"}
+    lens = prefill_lengths(32, seed=0)
+    p = prefill_case([(0, n) for n in lens], HQ, HKV, D, BS, torch.float16, seed=3, sentinel=False)
+    done_flops, t0, seqs = 0, time.perf_counter(), 0
+    for r, n in enumerate(lens):  # whole sequences in order until the budget is spent
+        sl = slice(r, r + 1)
+        ref.prefill_ref(p.q, p.k, p.v, p.tables[sl], p.starts[sl], p.q_lens[sl], p.ctx_lens[sl],
+                        p.scale, BS)  # fmt: skip
+        done_flops += 4 * HQ * D * n * (n + 1) // 2
+        seqs += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    res["prefill_varlen32_float16"] = {
+        "value": round(done_flops / dt / 1e12, 4), "unit": "TFLOP/s",
+        "sample": f"oracle.ref.prefill_ref on {seqs} of the 32 sequences ({done_flops / 1e9:.1f} GFLOP) "
+                  f"in {dt:.2f} s"}  # fmt: skip
+    f = fused_case(sentinel=False)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        ref.rms_norm(f.x, f.norm_w, f.eps)
+        ref.qk_norm_rope_store_ref(f.q, f.k, f.v, f.q_w, f.k_w, f.cos, f.sin, f.slots, f.k_cache, f.v_cache,
+                                   f.eps)  # fmt: skip
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s or reps >= 50:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    nbytes = 4096 * (1024 * 2 * 2 + 16904)
+    res["fused_t4096"] = {
+        "value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "ms": round(dt * 1e3, 2),
+        "sample": f"oracle.ref.rms_norm + qk_norm_rope_store_ref over the full T=4096 workload, "
+                  f"{reps} rep(s)"}  # fmt: skip
+    return res
+
+
+def kernel_name(plan: dict, dtype: str = "f16") -> str:
+    """The decode kernel instantiation the library dispatches for ``plan``."""
+    budget = {"heavy": "heavy", "light": "light", "light_stream": "light-stream"}[plan["budget"]]
+    return f"paged_attend_kernel<{dtype},{D},{plan['head_tile']},false,{budget}>"
 
 
 def batched_sdpa_prefill(p, out: torch.Tensor) -> torch.Tensor:
@@ -207,11 +265,22 @@ def batched_sdpa_prefill(p, out: torch.Tensor) -> torch.Tensor:
 def extra_measurements() -> dict:
     dev = torch.device("cuda:0")
     res: dict = {}
-    # Config 2: decode B=32 x 256, 4 splits (in-workgroup: one launch), a 4096-block pool.
+    # Config 2: decode B=32 x 256, a 4096-block pool: 4 splits + combine as the config
+    # states (fp32 partials in HBM and a second launch), and the policy's single launch
+    # (each sequence split over the waves of a workgroup, merged in LDS).
     c = decode_bench_case(32, 256, pool_blocks=4096, device=dev, seed=1)
-    ms = loop_ms(lambda: launch_paged_decode_split(*c.args(), c.scale, BS, num_splits=4), 200, 20)
     nb = decode_bytes(32, 256)["step"]
-    res["decode_b32_ctx256_s4"] = {"us": round(ms * 1e3, 2), "GB/s": round(nb / ms / 1e6, 1)}
+    for key, splits in (("decode_b32_ctx256_s4", 4), ("decode_b32_ctx256_policy", None)):
+        def call() -> None:
+            launch_paged_decode_split(*c.args(), c.scale, BS, num_splits=splits)
+
+        ms, ms_g = loop_ms(call, 200, 20), graph_ms(call)
+        plan = decode_plan(32, HQ, HKV, D, BS, c.block_tables.shape[1], splits or 1)
+        res[key] = {"us": round(ms * 1e3, 2), "GB/s": round(nb / ms / 1e6, 1),
+                    "graph_us": round(ms_g * 1e3, 2), "graph_GB/s": round(nb / ms_g / 1e6, 1),
+                    "launches": "split kernel + combine" if splits else "one launch",
+                    "kernel": kernel_name(plan), "grid": plan["grid"],
+                    "waves_per_group": plan["waves_per_group"]}  # fmt: skip
     # Config 3: varlen prefill, 32 prompts L ~ U[16, 2048], fp16 and bf16.
     lens = prefill_lengths(32, seed=0)
     flops = sum(4 * HQ * D * n * (n + 1) // 2 for n in lens)
@@ -359,10 +428,14 @@ def main() -> None:
     step_bytes, split_bytes = r["bytes"]["step"], r["bytes"]["split_kernel"]
     value = step_bytes / r["ms_per_step"] / 1e6  # GB/s
     achieved = split_bytes / r["split_ms"] / 1e6
-    traffic = None
+    # HBM bytes per launch come from the committed, calibrated rocprofv3 PMC run of this
+    # workload (FETCH_SIZE x 2 + WRITE_SIZE; a profiler cannot run inside this process).
+    traffic, traffic_src = None, None
     tf = ROOT / "profiles" / "paged_attend_decode_b64_ctx4096_traffic.json"
     if tf.exists() and (args.batch, args.ctx, splits) == (64, 4096, 1):
         traffic = json.loads(tf.read_text()).get("bytes_per_launch")
+        traffic_src = "profiles/paged_attend_decode_b64_ctx4096_traffic.json (rocprofv3 --pmc, calibrated)"
+    plan = decode_plan(args.batch, HQ, HKV, D, BS, nb, splits)
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -382,15 +455,19 @@ def main() -> None:
                                   else f"split-K {splits} + combine"),
                    "batch": args.batch, "ctx": args.ctx, "splits": splits,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "paged_attend_kernel<f16,128,2,false,light-stream>",
+        "roofline": {"bound": "hbm", "kernel": kernel_name(plan), "kernel_source": "ts_decode_plan",
+                     "launch": {"grid": plan["grid"], "waves_per_group": plan["waves_per_group"],
+                                "length_pairs": plan["by_length"]},
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "avg_launch_us": round(r["split_ms"] * 1e3, 2),
                      "algorithmic_bytes": split_bytes},
         "frac_of_peak_step": round(value / HBM_PEAK_GBS, 4),
     }  # fmt: skip
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(r["case"], splits)
+        line["cpu_baseline_other_configs"] = cpu_baselines_other_configs()
     if not args.no_extra:
         line["extra"] = extra_measurements()
     line.update(calibration_copies(args.copy_mb))

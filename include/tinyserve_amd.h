@@ -75,10 +75,12 @@ const char* ts_strerror(int code);
  * max_blocks: the width of block_tables (entries per row the caller filled, so every
  * context is at most max_blocks * block_size), or 0 if unknown. It only picks how the
  * launch runs: the register budget (short walks per wave run two waves per SIMD) and,
- * when the K/V it bounds exceeds 256 MiB, non-temporal K/V loads with one round of
- * two-wave-per-SIMD workgroups. Nothing is read by it, and a wrong value costs speed,
- * never correctness. (The reference passes the table to Triton and has no such
- * argument.)
+ * when the K/V it bounds exceeds 256 MiB (head dims 64 and 128), non-temporal K/V loads
+ * with one round of two-wave-per-SIMD workgroups. Nothing is read by it, and a wrong
+ * value costs speed, never correctness. Pass the tightest width known: a table padded to
+ * the model's maximum position (a graph captured for any context) bounds far more K/V
+ * than it holds, so every such launch takes the streaming shape, even at short contexts.
+ * (The reference passes the table to Triton and has no such argument.)
  */
 int ts_decode_split(const void* q, const void* k_cache, const void* v_cache,
                     const int32_t* block_tables, const int32_t* context_lens, void* out,
@@ -87,6 +89,16 @@ int ts_decode_split(const void* q, const void* k_cache, const void* v_cache,
                     int64_t o_stride_b, int64_t o_stride_h, int64_t k_stride_slot,
                     int64_t k_stride_head, int64_t bt_stride, int max_blocks, int splits,
                     int head_tile, float scale, int dtype, void* stream);
+
+/*
+ * The launch shape ts_decode_split picks for these sizes, without launching (a query for
+ * tests and benchmarks; no reference counterpart). Writes 8 ints to plan: the register
+ * budget (0 heavy: one wave per SIMD; 1 light: two per SIMD; 2 light with non-temporal
+ * K/V loads), waves per workgroup, 1 if workgroups take length pairs, query heads per
+ * wave, the grid's x, y, z, and the dynamic LDS bytes per workgroup.
+ */
+int ts_decode_plan(int B, int Hq, int Hkv, int D, int block_size, int max_blocks, int splits,
+                   int head_tile, int dtype, int* plan);
 
 /*
  * The split-K combine pass: out[b, h] = sum_s w_s acc_s / sum_s w_s l_s with

@@ -9,6 +9,7 @@ reads one slot too many returns NaN and fails. Tolerances: tests/helpers.py.
 
 from __future__ import annotations
 
+import math
 from collections.abc import Callable
 
 import pytest
@@ -17,7 +18,8 @@ from hypothesis import given, settings
 from hypothesis import strategies as st
 
 from oracle import ref
-from tests.helpers import TOL, assert_matches
+from tests.helpers import TOL, assert_contract, assert_matches
+from tinyserve_amd import _lib
 from tinyserve_amd import hip_attention as ha
 from tinyserve_amd.workloads import DecodeCase, decode_bench_case, decode_case
 
@@ -36,14 +38,15 @@ def oracle32(c: DecodeCase) -> torch.Tensor:
                           c.context_lens, c.scale, c.block_size)  # fmt: skip
 
 
-def check(c: DecodeCase, kernels: list[Callable[..., torch.Tensor]] = KERNELS) -> torch.Tensor:
+def check(c: DecodeCase, kernels: list[Callable[..., torch.Tensor]] = KERNELS,
+          contract: bool = False) -> torch.Tensor:  # fmt: skip
     want = oracle32(c)
     g = on_gpu(c)
     for kernel in kernels:
         out = kernel(*g.args(), g.scale, g.block_size)
         assert out.dtype == c.q.dtype and out.device.type == "cuda"
         assert torch.isfinite(out).all(), f"{kernel.__name__}: read a slot outside the sequence"
-        assert_matches(out, want, c.q.dtype, kernel.__name__)
+        (assert_contract if contract else assert_matches)(out, want, c.q.dtype, kernel.__name__)
     return want
 
 
@@ -62,7 +65,7 @@ def test_qwen3_shapes_across_block_boundaries() -> None:
 
 def test_baseline_config_1() -> None:
     # fp32, 16/8/128, contexts {17, 64, 128, 200}, a 64-block pool.
-    check(decode_case([17, 64, 128, 200], pool_blocks=64))
+    check(decode_case([17, 64, 128, 200], pool_blocks=64), contract=True)
 
 
 @pytest.mark.parametrize(("num_q_heads", "num_kv_heads"), [(4, 4), (8, 2), (8, 1), (16, 2)])
@@ -192,20 +195,65 @@ def test_benchmark_sized_batch() -> None:
 
 
 def test_baseline_config_2() -> None:
-    # fp16, B=32 at context 256, a 4096-block pool, 4 splits + combine.
+    # fp16, B=32 at context 256, a 4096-block pool, 4 splits + combine
+    # (the reference's ranges of ceil(16 / 4) = 4 blocks each write fp32 partials, and the
+    # combine pass finishes); and the policy's one launch (no count given), which splits
+    # each sequence over the waves of a workgroup instead.
     c = decode_case([256] * 32, dtype=torch.float16, pool_blocks=4096, seed=0)
     want = oracle32(c)
     g = on_gpu(c)
+    plan = ha.decode_plan(32, 16, 8, 128, 16, g.block_tables.shape[1], 4)
+    assert plan["grid"][2] == 4, plan
     out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, num_splits=4)
     assert torch.isfinite(out).all()
-    assert_matches(out, want, torch.float16)
+    assert_contract(out, want, torch.float16, "config 2, 4 splits + combine")
+    policy = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size)
+    assert_contract(policy, want, torch.float16, "config 2, policy (one launch)")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("splits,lens", [(4, [256] * 32), (16, [17, 300, 33, 1, 700, 2000]),
+                                         (3, [1, 2, 47, 48, 49]), (5, [64] * 3)])  # fmt: skip
+def test_split_partials_follow_the_reference_ranges(splits: int, lens: list[int], dtype: torch.dtype) -> None:
+    # ts_decode_split's fp32 partials, before the combine, against the oracle's restatement
+    # of _paged_decode_split_kernel (triton_attention.py:243-296): split s holds blocks
+    # [s * ceil(n / S), ...) of each sequence, empty past the end (m = -inf, l = 0). m is
+    # stored in base-2 units (log2 e * the max score).
+    c = decode_case(lens, dtype=dtype, seed=splits)
+    m_ref, l_ref, acc_ref = ref.split_partials_ref(c.q.float(), c.k_cache.float(), c.v_cache.float(),
+                                                   c.block_tables, c.context_lens, c.scale, c.block_size,
+                                                   splits)  # fmt: skip
+    g = on_gpu(c)
+    b, hq, d = g.q.shape
+    m = torch.empty((b, hq, splits), dtype=torch.float32, device=DEVICE)
+    l = torch.empty_like(m)  # noqa: E741
+    acc = torch.empty((b, hq, splits, d), dtype=torch.float32, device=DEVICE)
+    _lib.call("ts_decode_split", g.q.data_ptr(), g.k_cache.data_ptr(), g.v_cache.data_ptr(),
+              g.block_tables.data_ptr(), g.context_lens.data_ptr(), None, m.data_ptr(), l.data_ptr(),
+              acc.data_ptr(), b, hq, g.k_cache.shape[1], d, g.block_size, g.q.stride(0), g.q.stride(1),
+              0, 0, g.k_cache.stride(0), g.k_cache.stride(1), g.block_tables.stride(0),
+              g.block_tables.shape[1], splits, 0, g.scale, _lib.dtype_code(g.q),
+              _lib.stream_of(0))  # fmt: skip
+    torch.cuda.synchronize()
+    m, l, acc = m.cpu(), l.cpu(), acc.cpu()  # noqa: E741
+    empty = m_ref == float("-inf")
+    assert torch.equal(m == float("-inf"), empty) and bool((l[empty] == 0).all())
+    assert bool((acc[empty] == 0).all())
+    full = ~empty
+    torch.testing.assert_close(m[full] * math.log(2.0), m_ref[full], atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(l[full], l_ref[full], atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(acc[full], acc_ref[full], atol=1e-4, rtol=1e-5)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_metric_size_batch(dtype: torch.dtype) -> None:
-    # The metric's workload, B=64 x 4096, fp16/bf16: 8 of the 64 sequences against the
-    # oracle, every sequence for split-count invariance (1 vs 8 vs 16 splits).
+    # The metric's workload, B=64 x 4096, fp16/bf16. The benched launch (one split: the
+    # streaming budget on length pairs, a single launch) against the oracle on 8 of the
+    # 64 sequences at the contract's bound, and every sequence for split-count
+    # invariance (1 vs 8 vs 16 HBM splits).
     c = decode_bench_case(64, 4096, dtype=dtype, seed=5)
+    plan = ha.decode_plan(64, 16, 8, 128, 16, c.block_tables.shape[1], 1, dtype=dtype)
+    assert plan["budget"] == "light_stream" and plan["by_length"], plan
     outs = {s: ha.launch_paged_decode_split(*c.args(), c.scale, c.block_size, num_splits=s)
             for s in (1, 8, 16)}  # fmt: skip
     for s, out in outs.items():
@@ -214,10 +262,12 @@ def test_metric_size_batch(dtype: torch.dtype) -> None:
     torch.testing.assert_close(outs[8], outs[1], atol=tol, rtol=tol)
     torch.testing.assert_close(outs[16], outs[1], atol=tol, rtol=tol)
     kc, vc = c.k_cache.cpu(), c.v_cache.cpu()
-    for b in range(0, 64, 8):
-        sub = DecodeCase(c.q[b : b + 1].cpu(), kc, vc, c.block_tables[b : b + 1].cpu(),
-                         c.context_lens[b : b + 1].cpu(), c.scale, c.block_size)  # fmt: skip
-        assert_matches(outs[8][b : b + 1], oracle32(sub), dtype, f"seq {b}")
+    rows = list(range(0, 64, 8))
+    sub = DecodeCase(c.q[rows].cpu(), kc, vc, c.block_tables[rows].cpu(), c.context_lens[rows].cpu(),
+                     c.scale, c.block_size)  # fmt: skip
+    want = oracle32(sub)
+    assert_contract(outs[1][rows], want, dtype, "metric size, the benched one-split launch")
+    assert_contract(outs[8][rows], want, dtype, "metric size, 8 splits + combine")
 
 
 @pytest.mark.parametrize("batch", [20, 40, 80])
@@ -335,13 +385,16 @@ def test_launches_of_several_rounds(batch: int, splits: int, head_dim: int, dtyp
 
 @pytest.mark.parametrize("splits", [2, 3, 4])
 def test_partials_and_combine_at_small_split_counts(splits: int) -> None:
-    # launch_paged_decode_split runs up to 4 splits inside one workgroup; the C entry's
-    # HBM-partial + combine path at those counts is checked here directly.
+    # An explicit count of 2-4 splits runs as HBM partials plus the combine (the policy
+    # alone turns such counts into one launch split over a workgroup's waves).
     c = decode_case([17, 300, 33, 1], dtype=torch.float16, seed=splits)
     want = oracle32(c)
     g = on_gpu(c)
-    out = ha._launch(*g.args(), g.scale, g.block_size, splits, 0)
+    assert ha.decode_plan(4, 16, 8, 128, 16, g.block_tables.shape[1], splits)["grid"][2] == splits
+    out = ha.launch_paged_decode_split(*g.args(), g.scale, g.block_size, num_splits=splits)
     assert_matches(out, want, torch.float16, f"splits={splits}")
+    policy = ha.launch_paged_decode_split(*g.args(), g.scale, g.block_size)
+    assert_matches(policy, want, torch.float16, "policy")
 
 
 @pytest.mark.parametrize("splits", [9, 64, 65, 130])
@@ -363,22 +416,44 @@ def test_combine_over_many_splits(splits: int, head_dim: int, dtype: torch.dtype
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("head_dim", [64, 128])
-def test_streaming_launches(dtype: torch.dtype, head_dim: int) -> None:
+@pytest.mark.parametrize("heads,head_tile", [((16, 8), 0), ((32, 8), 0), ((8, 8), 0), ((16, 8), 1)])
+def test_streaming_launches(dtype: torch.dtype, head_dim: int, heads: tuple[int, int], head_tile: int) -> None:
     # A table wide enough to bound more than 256 MiB of K/V makes the launch stream K/V
-    # with non-temporal loads (light budget, one round of workgroups, no length pairs);
-    # the unused columns are never read. The results match the oracle and the launch
-    # over the tight table, for one split and for HBM splits.
+    # with non-temporal loads (light budget, one round of workgroups); the unused columns
+    # are never read. Head groups of 2, 4 and 1 (tiles of 2, 4 and 1 query heads) and the
+    # per-head launch; 32 sequences give length pairs at one split. The results match the
+    # oracle and the launch over the tight table, for one split and for HBM splits.
     lens = [1, 17, 300, 64, 1000, 5, 700, 33] * 4
-    c = decode_case(lens, head_dim=head_dim, dtype=dtype, seed=11)
+    c = decode_case(lens, *heads, head_dim=head_dim, dtype=dtype, seed=11)
     want = oracle32(c)
     g = on_gpu(c)
     b, w = g.block_tables.shape
     wide = torch.full((b, 8192), -1, dtype=torch.int32, device=DEVICE)  # -1: never read
     wide[:, :w] = g.block_tables
     for splits in (1, 4):
-        tight = ha.launch_paged_decode_split(*g.args(), g.scale, g.block_size, num_splits=splits)
-        out = ha.launch_paged_decode_split(g.q, g.k_cache, g.v_cache, wide, g.context_lens, g.scale,
-                                           g.block_size, num_splits=splits)  # fmt: skip
+        plan = ha.decode_plan(b, *heads, head_dim, g.block_size, 8192, splits, head_tile, dtype)
+        assert plan["budget"] == "light_stream", plan
+        tight = ha._launch(*g.args(), g.scale, g.block_size, splits, head_tile)
+        out = ha._launch(g.q, g.k_cache, g.v_cache, wide, g.context_lens, g.scale, g.block_size, splits,
+                         head_tile)  # fmt: skip
         assert torch.isfinite(out).all(), splits
         assert_matches(out, want, dtype, f"streaming, {splits} split(s)")
         torch.testing.assert_close(out, tight, atol=TOL[dtype], rtol=TOL[dtype])
+
+
+def test_streaming_threshold() -> None:
+    # bf16, 64 sequences, 8 kv heads of 128: each table column bounds 64 x 16 x 4 KiB =
+    # 4 MiB of K/V, so a width of 64 bounds exactly 256 MiB (cached loads) and 65 just
+    # over it (streaming). Both give the oracle's result on the same sequences.
+    lens = [1 + (389 * i) % 1024 for i in range(64)]
+    c = decode_case(lens, dtype=torch.bfloat16, seed=13)
+    want = oracle32(c)
+    g = on_gpu(c)
+    assert int(g.context_lens.max()) <= 64 * 16  # every sequence fits a 64-column table
+    assert ha.decode_plan(64, 16, 8, 128, 16, 64, 1, dtype=torch.bfloat16)["budget"] != "light_stream"
+    assert ha.decode_plan(64, 16, 8, 128, 16, 65, 1, dtype=torch.bfloat16)["budget"] == "light_stream"
+    for width in (64, 65):
+        tables = widened(g.block_tables, width)
+        out = ha.launch_paged_decode_split(g.q, g.k_cache, g.v_cache, tables, g.context_lens, g.scale,
+                                           g.block_size, num_splits=1)  # fmt: skip
+        assert_matches(out, want, torch.bfloat16, f"width {width}")

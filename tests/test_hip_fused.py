@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from oracle import ref
-from tests.helpers import ULP, assert_matches
+from tests.helpers import ULP, assert_contract, assert_matches
 from tinyserve_amd.hip_fused import qk_norm_rope_store, rms_norm_rows
 from tinyserve_amd.workloads import fused_case
 
@@ -123,18 +123,21 @@ def test_qk_norm_rope_store_into_a_float32_cache() -> None:
 def test_baseline_config_4(dtype: torch.dtype) -> None:
     # T=4096, hidden 1024, q/k/v as strided views of the QKV
     # projection output, an injective slot map into a 512 x 16 pool; scatter bit-exact.
+    # Values within the contract's max-abs bound (fp16 2e-3), except where the rounding
+    # of x/rms to the input dtype (layers.py:34-38) lands on the other neighbour of a
+    # near-tie: one ulp of that intermediate, rare, allowed by ``extra``.
     cpu = fused_case(dtype=dtype, device="cpu")
     dev = fused_case(dtype=dtype, device=DEVICE)
     x = rms_norm_rows(dev.x, dev.norm_w, dev.eps)
     want, extra = rms32(cpu.x, cpu.norm_w)
-    assert_matches(x, want, dtype, "rms_norm_rows", extra)
+    assert_contract(x, want, dtype, "config 4 rms_norm_rows", extra)
     q = qk_norm_rope_store(dev.q, dev.k, dev.v, dev.q_w, dev.k_w, dev.cos, dev.sin, dev.slots,
                            dev.k_cache, dev.v_cache, dev.eps)  # fmt: skip
     want_q, extra_q = rope32(cpu.q, cpu.q_w, cpu.cos, cpu.sin)
-    assert_matches(q, want_q, dtype, "q", extra_q)
+    assert_contract(q, want_q, dtype, "config 4 q", extra_q)
     kc, vc = dev.k_cache.cpu(), dev.v_cache.cpu()
     want_k, extra_k = rope32(cpu.k, cpu.k_w, cpu.cos, cpu.sin)
-    assert_matches(kc[cpu.slots], want_k, dtype, "k", extra_k)
+    assert_contract(kc[cpu.slots], want_k, dtype, "config 4 k", extra_k)
     assert torch.equal(vc[cpu.slots], cpu.v)
     # Placement: the oracle's KVCache.write of the kernel's own k rows lands bit-identically.
     kc_ref = torch.full_like(kc, float("nan"))

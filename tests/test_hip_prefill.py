@@ -16,7 +16,7 @@ from hypothesis import given, settings
 from hypothesis import strategies as st
 
 from oracle import ref
-from tests.helpers import assert_matches
+from tests.helpers import assert_contract, assert_matches
 from tinyserve_amd.hip_prefill import paged_prefill_attention
 from tinyserve_amd.workloads import PrefillCase, prefill_case, prefill_lengths
 
@@ -145,10 +145,30 @@ def test_qwen3_shapes_with_prefix_hits(dtype: torch.dtype) -> None:
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_baseline_config_3(dtype: torch.dtype) -> None:
-    # 32 fresh prompts, L ~ U[16, 2048], packed by cu_seqlens.
+    # 32 fresh prompts, L ~ U[16, 2048], packed by cu_seqlens; every
+    # row within the contract's max-abs bound against the per-sequence oracle (fp16: 2e-3
+    # including P's rounding to fp16 before P.V, as triton_prefill.py:118 rounds it).
     lens = prefill_lengths(32, seed=0)
     c = prefill_case([(0, n) for n in lens], 16, 8, 128, 16, dtype, seed=3)
-    check(c, run(c))
+    out = run(c)
+    check(c, out)
+    assert_contract(out, oracle32(c), dtype, "config 3")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_baseline_config_3_against_the_batched_path(dtype: torch.dtype) -> None:
+    # The reference's other prefill path, prefill_plan + batched_prefill_attention
+    # (attention.py:144-220): every sequence padded into one rectangle and attended by one
+    # masked float32 SDPA call, run here on the GPU on config 3's inputs. Its padding keys
+    # read slot 0 under the mask (as the reference's plan pads them), so the pool holds no
+    # NaN sentinels here: 0 x NaN would poison the masked sum.
+    lens = prefill_lengths(32, seed=0)
+    c = prefill_case([(0, n) for n in lens], 16, 8, 128, 16, dtype, seed=3, sentinel=False)
+    g = on_gpu(c)
+    out = run(c)
+    want = ref.batched_prefill_ref(g.q, g.k, g.v, g.tables, g.starts, g.q_lens, g.ctx_lens, g.scale,
+                                   g.block_size, out=torch.empty_like(g.q, dtype=torch.float32))  # fmt: skip
+    assert_contract(out, want, dtype, "config 3 vs the batched SDPA path")
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

@@ -67,6 +67,26 @@ def test_c_abi_rejects_bad_sizes_before_any_launch(lib: ctypes.CDLL) -> None:
     assert lib.ts_rms_norm_rows(null, null, null, 0, 16, 16, 16, 1e-6, 1, null) == 0
 
 
+def test_decode_launch_plans(lib: ctypes.CDLL) -> None:
+    # The launch shape is a function of sizes only (MI355X: 256 CUs; without a device the
+    # library assumes that count). The metric's B=64 x 4096 streams K/V on length pairs of
+    # 8 waves; an explicit count of 4 splits (config 2) runs 4 ranges in the grid's z;
+    # head dims without a non-temporal kernel (256) keep cached loads however wide the
+    # table; the policy's one launch at config 2 is one 8-wave workgroup per
+    # (sequence, head tile).
+    plan = hip_attention.decode_plan
+    assert plan(64, 16, 8, 128, 16, 256, 1) == {
+        "budget": "light_stream", "waves_per_group": 8, "by_length": True, "head_tile": 2,
+        "grid": (8, 32, 1), "lds_bytes": 2 * 8 * 2 * 130 * 4}  # fmt: skip
+    assert plan(32, 16, 8, 128, 16, 16, 4)["grid"] == (8, 32, 4)
+    assert plan(32, 16, 8, 128, 16, 16, 1)["waves_per_group"] == 8
+    assert plan(64, 16, 8, 256, 16, 2560, 1)["budget"] == "heavy"
+    assert plan(64, 16, 8, 128, 16, 2560, 16)["budget"] == "light_stream"
+    assert plan(8, 32, 8, 128, 16, 8, 1, head_tile=1)["head_tile"] == 1
+    with pytest.raises(ValueError):
+        plan(8, 12, 8, 128, 16, 8, 1)
+
+
 # --- decode entry points: the reference's argument errors (test_triton_attention.py:201-234)
 
 

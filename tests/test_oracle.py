@@ -125,6 +125,38 @@ def test_decode_ref_one_token_returns_its_value() -> None:  # test_triton_attent
     torch.testing.assert_close(out[0], vc[48].repeat_interleave(2, dim=0))
 
 
+def test_split_partials_hand_computed() -> None:  # triton_attention.py:283-296
+    # Two tokens, one per block, two splits: each range holds one key, so m is that key's
+    # score, l = 1 and acc is its value. A third split is past the end: empty.
+    q = torch.tensor([[[1.0, 2.0]]])
+    kc = torch.tensor([[[0.5, 0.0]], [[1.0, 1.0]], [[9.0, 9.0]]])
+    vc = torch.tensor([[[3.0, 4.0]], [[5.0, 6.0]], [[7.0, 8.0]]])
+    tables = torch.tensor([[2, 1]], dtype=torch.int32)  # block size 1: slots 2, 1
+    m, l, acc = ref.split_partials_ref(q, kc, vc, tables, torch.tensor([2], dtype=torch.int32), 0.5, 1, 3)  # noqa: E741
+    assert m[0, 0].tolist() == [13.5, 1.5, float("-inf")]
+    assert l[0, 0].tolist() == [1.0, 1.0, 0.0]
+    assert acc[0, 0].tolist() == [[7.0, 8.0], [5.0, 6.0], [0.0, 0.0]]
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 40])
+def test_split_partials_merge_to_the_decode(splits: int) -> None:
+    # Any split count merges to the unsplit attention; ranges follow ceil(n / S) blocks,
+    # so 40 ranges over at most 19 blocks leave trailing ones empty (m = -inf, l = 0).
+    kc, vc = rand(96, 2, 8, seed=3), rand(96, 2, 8, seed=4)
+    q = rand(3, 4, 8, seed=5)
+    tables = torch.randperm(24, generator=torch.Generator().manual_seed(6)).to(torch.int32).view(3, 8)
+    lens = torch.tensor([1, 19, 30], dtype=torch.int32)
+    m, l, acc = ref.split_partials_ref(q, kc, vc, tables, lens, 0.3, 4, splits)  # noqa: E741
+    want = ref.decode_ref(q, kc, vc, tables, lens, 0.3, 4)
+    torch.testing.assert_close(ref.merge_partials_ref(m, l, acc), want)
+    for b, n in enumerate(lens.tolist()):
+        nblocks = -(-n // 4)
+        per = -(-nblocks // splits)
+        used = -(-nblocks // per)  # ranges holding at least one block
+        assert torch.isfinite(m[b, :, :used]).all() and (l[b, :, :used] >= 1.0).all()
+        assert (m[b, :, used:] == float("-inf")).all() and (l[b, :, used:] == 0).all()
+
+
 def test_prefill_ref_is_per_sequence_and_leaves_other_rows() -> None:
     kc, vc = rand(64, 2, 8, seed=1), rand(64, 2, 8, seed=2)
     tables = torch.tensor([[5, 9, 0], [2, 3, 0]], dtype=torch.int32)

@@ -35,6 +35,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i64, _i64, _i64, _i64, _i64, _i64, _i64,  # strides
          _i, _i, _i, _f, _i, _vp],  # max_blocks splits head_tile scale dtype stream
     ),
+    "ts_decode_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _i, _c_i32p]),
     "ts_decode_combine": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i64, _i, _i, _vp]),
     "ts_prefill_varlen": (
         _i,

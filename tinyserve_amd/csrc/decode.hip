@@ -163,43 +163,65 @@ __device__ __forceinline__ void merge_token_lanes(TokenState<T, D, HT, LB>& st) 
 constexpr int kMaxWavesPerGroup = 4;  // heavy budget, and length pairs
 constexpr int kMaxWavesLight = 8;     // light budget (two waves per SIMD)
 
-// The W waves of a decode workgroup each hold a merged state (in their first LPT lanes,
-// lane c holding elements (i * LPT + c) * VEC + j). They park it in LDS, then thread t
-// of the group produces output element t (of HT * D) by the two-partial rule over the W
-// states, and writes it either as the final output (one split) or as the split's fp32
-// partial for the combine pass.
-template <typename T, int D, int HT, int MAXW, typename State, typename Args>
-__device__ __forceinline__ void merge_group_waves(const Args& a, const State& st, int wave,
-                                                  int c, int seq, int h0, int split,
-                                                  int64_t orow) {
+// LDS of a decode workgroup (dynamic, sized by the launch): NS state slots, each the
+// HT maxima, HT denominators and HT x D accumulators of one wave's merged state. A plain
+// workgroup of W > 1 waves parks one state per wave (NS = W); a length pair parks up to
+// two per wave, one per sequence it walked (NS = 2W, slot 2w + i). One-wave workgroups
+// take none.
+template <int HT, int D>
+struct StateSlots {
+  float* base;
+  int ns;
+  __device__ float& m(int s, int g) const { return base[s * HT + g]; }
+  __device__ float& l(int s, int g) const { return base[(ns + s) * HT + g]; }
+  __device__ float& acc(int s, int g, int d) const { return base[2 * ns * HT + (s * HT + g) * D + d]; }
+};
+
+__host__ __device__ constexpr int64_t state_slot_bytes(int ht, int d) {
+  return static_cast<int64_t>(ht) * (d + 2) * 4;
+}
+
+// Lanes c (c >= 0: the first LPT lanes of a wave, lane c holding elements
+// (i * LPT + c) * VEC + j) write their merged state to slot s.
+template <typename State, typename Slots>
+__device__ __forceinline__ void park_state(const Slots& ss, const State& st, int s, int c) {
   using S = typename State::S;
   constexpr int NV = S::kNV, VEC = S::kVec, LPT = S::kLPT;
-  __shared__ float sm[MAXW][HT], sl[MAXW][HT];
-  __shared__ float sacc[MAXW][HT][D];
-  if (c >= 0) {
+  constexpr int HT = sizeof(st.m) / sizeof(float);
+  if (c < 0) return;
 #pragma unroll
-    for (int g = 0; g < HT; ++g) {
-      if (c == 0) {
-        sm[wave][g] = st.m[g];
-        sl[wave][g] = st.l[g];
-      }
-#pragma unroll
-      for (int i = 0; i < NV; ++i)
-#pragma unroll
-        for (int j = 0; j < VEC; ++j) sacc[wave][g][(i * LPT + c) * VEC + j] = st.acc[g][i * VEC + j];
+  for (int g = 0; g < HT; ++g) {
+    if (c == 0) {
+      ss.m(s, g) = st.m[g];
+      ss.l(s, g) = st.l[g];
     }
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) ss.acc(s, g, (i * LPT + c) * VEC + j) = st.acc[g][i * VEC + j];
   }
+}
+
+// The W waves of a decode workgroup each hold a merged state. They park it in LDS, then
+// thread t of the group produces output element t (of HT * D) by the two-partial rule
+// over the W states, and writes it either as the final output (one split) or as the
+// split's fp32 partial for the combine pass.
+template <typename T, int D, int HT, typename State, typename Args>
+__device__ __forceinline__ void merge_group_waves(const Args& a, const StateSlots<HT, D>& ss,
+                                                  const State& st, int wave, int c, int seq,
+                                                  int h0, int split, int64_t orow) {
+  park_state(ss, st, wave, c);
   __syncthreads();
   const int W = a.wpg;
   for (int t = threadIdx.x; t < HT * D; t += W * kWave) {
     const int g = t / D, d = t % D;
-    float mm = sm[0][g];
-    for (int w = 1; w < W; ++w) mm = fmaxf(mm, sm[w][g]);
+    float mm = ss.m(0, g);
+    for (int w = 1; w < W; ++w) mm = fmaxf(mm, ss.m(w, g));
     float den = 0.f, num = 0.f;
     for (int w = 0; w < W; ++w) {
-      const float f = fast_exp2(sm[w][g] - mm);
-      den = fmaf(f, sl[w][g], den);
-      num = fmaf(f, sacc[w][g][d], num);
+      const float f = fast_exp2(ss.m(w, g) - mm);
+      den = fmaf(f, ss.l(w, g), den);
+      num = fmaf(f, ss.acc(w, g, d), num);
     }
     if (a.splits == 1) {
       static_cast<T*>(a.out)[orow + (h0 + g) * a.o_sh + d] = from_f32<T>(num / den);
@@ -217,34 +239,6 @@ __device__ __forceinline__ void merge_group_waves(const Args& a, const State& st
 // A finite "no score yet" maximum: 2^(kNoMax - real score) is exactly 0, and two empty
 // states merge to an empty state without inf - inf.
 constexpr float kNoMax = -1.0e30f;
-
-// A workgroup of a length pair (one split): each wave parks up to two merged states, one
-// per sequence it walked, in walking order (slot 0, then slot 1), then thread t of the
-// group produces element t of each sequence's output over the waves that walked it.
-template <typename T, int D, int HT>
-struct PairSlots {
-  float m[kMaxWavesPerGroup][2][HT], l[kMaxWavesPerGroup][2][HT];
-  float acc[kMaxWavesPerGroup][2][HT][D];
-};
-
-template <typename T, int D, int HT, typename State>
-__device__ __forceinline__ void park_state(PairSlots<T, D, HT>& ps, const State& st, int wave,
-                                           int slot, int c) {
-  using S = typename State::S;
-  constexpr int NV = S::kNV, VEC = S::kVec, LPT = S::kLPT;
-  if (c < 0) return;
-#pragma unroll
-  for (int g = 0; g < HT; ++g) {
-    if (c == 0) {
-      ps.m[wave][slot][g] = st.m[g];
-      ps.l[wave][slot][g] = st.l[g];
-    }
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-#pragma unroll
-      for (int j = 0; j < VEC; ++j) ps.acc[wave][slot][g][(i * LPT + c) * VEC + j] = st.acc[g][i * VEC + j];
-  }
-}
 
 template <typename T, int D, int HT, bool PREFILL, int BUDGET>
 __global__ __launch_bounds__(PREFILL ? kWave : kWave * (BudgetOf<BUDGET>::kLightish ? kMaxWavesLight : kMaxWavesPerGroup))
@@ -335,16 +329,23 @@ void paged_attend_kernel(const AttendArgs a) {
   const int lbs = a.lbs;
   const int bs_mask = (1 << lbs) - 1;
   const int nblocks = (ctx + bs_mask) >> lbs;
-  const int ranges = a.splits * (PREFILL ? 1 : a.wpg);
-  const int per = (nblocks + ranges - 1) / ranges;
-  int first = (split * (PREFILL ? 1 : a.wpg) + wave) * per;
-  int last = min(first + per, nblocks);
+  // Split s covers blocks [s * ceil(n / S), ...) of the sequence, clipped to n (the
+  // reference's ranges, triton_attention.py:283-286, so each partial holds the same
+  // keys); the W waves of its workgroup take equal contiguous shares of that range.
+  const int per_split = (nblocks + a.splits - 1) / a.splits;
+  const int s_first = min(split * per_split, nblocks);
+  const int s_last = min(s_first + per_split, nblocks);
+  const int nw = PREFILL ? 1 : a.wpg;
+  const int per = (s_last - s_first + nw - 1) / nw;
+  int first = s_first + wave * per;
+  int last = min(first + per, s_last);
   bool pair = false;
   if constexpr (!PREFILL) pair = a.by_length;
   if (!pair) seg_seq[0] = seq, seg_first[0] = first, seg_last[0] = last;
 
   TokenState<T, D, HT, LB> st;
-  __shared__ PairSlots<T, D, HT> pslots;
+  extern __shared__ float lds_slots[];
+  const StateSlots<HT, D> ss{lds_slots, (pair ? 2 : 1) * (PREFILL ? 1 : a.wpg)};
   for (int sgi = 0; sgi < nseg; ++sgi) {
   if (pair) {
     seq = seg_seq[sgi];
@@ -461,7 +462,7 @@ void paged_attend_kernel(const AttendArgs a) {
   }
 
   merge_token_lanes(st);
-  if (pair) park_state(pslots, st, wave, sgi, tl == 0 ? c : -1);
+  if (pair) park_state(ss, st, 2 * wave + sgi, tl == 0 ? c : -1);
   }  // segments
   if constexpr (!PREFILL) {
     if (pair) {
@@ -477,13 +478,13 @@ void paged_attend_kernel(const AttendArgs a) {
         const int g = (t % (HT * D)) / D, d = t % D;
         const int w0 = pi ? wb : 0, w1 = pi ? W : wa;
         float mm = kNoMax;
-        for (int w = w0; w < w1; ++w) mm = fmaxf(mm, pslots.m[w][pi && w * share < n_a][g]);
+        for (int w = w0; w < w1; ++w) mm = fmaxf(mm, ss.m(2 * w + (pi && w * share < n_a), g));
         float den = 0.f, num = 0.f;
         for (int w = w0; w < w1; ++w) {
-          const int sl = pi && w * share < n_a;
-          const float f = fast_exp2(pslots.m[w][sl][g] - mm);
-          den = fmaf(f, pslots.l[w][sl][g], den);
-          num = fmaf(f, pslots.acc[w][sl][g][d], num);
+          const int sl = 2 * w + (pi && w * share < n_a);
+          const float f = fast_exp2(ss.m(sl, g) - mm);
+          den = fmaf(f, ss.l(sl, g), den);
+          num = fmaf(f, ss.acc(sl, g, d), num);
         }
         const int64_t row = static_cast<int64_t>(pi ? pair_b : pair_a) * a.o_sb;
         static_cast<T*>(a.out)[row + (h0 + g) * a.o_sh + d] = from_f32<T>(num / den);
@@ -491,8 +492,7 @@ void paged_attend_kernel(const AttendArgs a) {
       return;
     }
     if (a.wpg > 1) {
-      merge_group_waves<T, D, HT, BudgetOf<BUDGET>::kLightish ? kMaxWavesLight : kMaxWavesPerGroup>(
-          a, st, wave, tl == 0 ? c : -1, seq, h0, split, orow);
+      merge_group_waves<T, D, HT>(a, ss, st, wave, tl == 0 ? c : -1, seq, h0, split, orow);
       return;
     }
   }
@@ -595,34 +595,35 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ m
 }
 
 template <typename T, int D, int HT, bool PREFILL>
-static int launch_attend(const AttendArgs& a, dim3 grid, bool light, hipStream_t stream) {
+static int launch_attend(const AttendArgs& a, dim3 grid, bool light, size_t lds, hipStream_t stream) {
   {
     if constexpr (!PREFILL && (D == 64 || D == 128)) {
       if (light && a.stream_kv) {
         hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, PREFILL, kLightStream>), grid,
-                           dim3(kWave * a.wpg), 0, stream, a);
+                           dim3(kWave * a.wpg), lds, stream, a);
         return launch_status();
       }
     }
     if (light) {
       hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, PREFILL, kLight>), grid,
-                         dim3(kWave * a.wpg), 0, stream, a);
+                         dim3(kWave * a.wpg), lds, stream, a);
       return launch_status();
     }
   }
   hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, PREFILL, kHeavy>), grid, dim3(kWave * a.wpg),
-                     0, stream, a);
+                     lds, stream, a);
   return launch_status();
 }
 
 template <typename T, bool PREFILL>
-static int dispatch_d(const AttendArgs& a, int D, int ht, dim3 grid, bool light, hipStream_t stream) {
-#define TS_HT(DD)                                                           \
-  switch (ht) {                                                             \
-    case 1: return launch_attend<T, DD, 1, PREFILL>(a, grid, light, stream); \
-    case 2: return launch_attend<T, DD, 2, PREFILL>(a, grid, light, stream); \
-    case 4: return launch_attend<T, DD, 4, PREFILL>(a, grid, light, stream); \
-    default: return TS_EUNSUPPORTED;                                        \
+static int dispatch_d(const AttendArgs& a, int D, int ht, dim3 grid, bool light, size_t lds,
+                      hipStream_t stream) {
+#define TS_HT(DD)                                                                \
+  switch (ht) {                                                                  \
+    case 1: return launch_attend<T, DD, 1, PREFILL>(a, grid, light, lds, stream); \
+    case 2: return launch_attend<T, DD, 2, PREFILL>(a, grid, light, lds, stream); \
+    case 4: return launch_attend<T, DD, 4, PREFILL>(a, grid, light, lds, stream); \
+    default: return TS_EUNSUPPORTED;                                             \
   }
   switch (D) {
     case 8: TS_HT(8)
@@ -645,11 +646,11 @@ static bool light_budget(int64_t waves, bool short_walks) {
 
 template <bool PREFILL>
 static int dispatch_attend(const AttendArgs& a, int dtype, int D, int ht, dim3 grid,
-                           bool light, hipStream_t stream) {
+                           bool light, size_t lds, hipStream_t stream) {
   switch (dtype) {
-    case TS_F32: return dispatch_d<float, PREFILL>(a, D, ht, grid, light, stream);
-    case TS_F16: return dispatch_d<f16, PREFILL>(a, D, ht, grid, light, stream);
-    case TS_BF16: return dispatch_d<bf16, PREFILL>(a, D, ht, grid, light, stream);
+    case TS_F32: return dispatch_d<float, PREFILL>(a, D, ht, grid, light, lds, stream);
+    case TS_F16: return dispatch_d<f16, PREFILL>(a, D, ht, grid, light, lds, stream);
+    case TS_BF16: return dispatch_d<bf16, PREFILL>(a, D, ht, grid, light, lds, stream);
     default: return TS_EUNSUPPORTED;
   }
 }
@@ -678,7 +679,7 @@ int prefill_rows_generic(const void* q, const void* k, const void* v, void* out,
                scale * kLog2e};
   dim3 grid(static_cast<unsigned>(R) * max_q_len, Hq / ht, 1);
   const int64_t waves = static_cast<int64_t>(grid.x) * grid.y;
-  return dispatch_attend<true>(a, dtype, D, ht, grid, light_budget(waves, false), stream);
+  return dispatch_attend<true>(a, dtype, D, ht, grid, light_budget(waves, false), 0, stream);
 }
 
 template <typename T>
@@ -699,20 +700,23 @@ static int launch_combine(const float* m, const float* l, const float* acc, T* o
 
 using namespace ts;
 
-extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v_cache,
-                               const int32_t* block_tables, const int32_t* context_lens,
-                               void* out, float* m, float* l, float* acc, int B, int Hq,
-                               int Hkv, int D, int block_size, int64_t q_stride_b,
-                               int64_t q_stride_h, int64_t o_stride_b, int64_t o_stride_h,
-                               int64_t k_stride_slot, int64_t k_stride_head, int64_t bt_stride,
-                               int max_blocks, int splits, int head_tile, float scale, int dtype,
-                               void* stream) {
-  if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || splits < 1 || !is_pow2(block_size))
+namespace ts {
+
+// The launch shape of one decode call, from shapes only (never from lengths, so a
+// captured graph always launches the same grid).
+struct DecodePlan {
+  int ht;         // query heads per wave
+  int wpg;        // waves per workgroup
+  int by_length;  // workgroups take length pairs
+  int budget;     // kHeavy, kLight or kLightStream
+  dim3 grid;
+  size_t lds;     // dynamic LDS bytes
+};
+
+static int plan_decode(int B, int Hq, int Hkv, int D, int block_size, int max_blocks, int splits,
+                       int head_tile, int dtype, DecodePlan* plan) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || splits < 1 || !is_pow2(block_size))
     return TS_EINVAL;
-  if (B == 0) return 0;
-  if (B > 65535) return TS_EUNSUPPORTED;  // sequences are the grid's y dimension
-  if (splits > 1 && (!m || !l || !acc)) return TS_EINVAL;
-  if (splits == 1 && !out) return TS_EINVAL;
   const int group = Hq / Hkv;
   const int ht = head_tile_for(group, head_tile);
   if (ht < 0) return TS_EINVAL;
@@ -737,33 +741,78 @@ extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v
   // K/V (bounded by the table width) larger than the 256 MiB last-level cache: it is read
   // once, so it goes through non-temporal loads (caching it only evicts other lines), under
   // the light budget, in workgroups of up to 8 waves sized for one round of the chip
-  // (8 waves per CU), without length pairs. Measured against the heavy one-round launch:
-  // +13% to +16.5% at 64 x 4096 (189.6 -> 164.9 us, 6.5 TB/s), 32 x 4096, 64 x 2048,
-  // 16 x 8192 and 128 x 4096; -4.8% for 64 mixed lengths in U[1024, 4096], which lose
-  // their pairs. Smaller launches keep cached loads, which let K/V that a previous step
-  // left in the cache be read from there (32 x 256: -13% with non-temporal loads).
+  // (8 waves per CU); length pairs then take 8 waves, so each sequence of a pair keeps
+  // about 4. Measured against the heavy one-round launch: +13% to +16.5% at 64 x 4096
+  // (189.6 -> 164.9 us, 6.5 TB/s), 32 x 4096, 64 x 2048, 16 x 8192 and 128 x 4096.
+  // Smaller launches keep cached loads, which let K/V that a previous step left in the
+  // cache be read from there (32 x 256: -13% with non-temporal loads). The non-temporal
+  // instantiation exists for head rows of 64 and 128 elements only; other head dims keep
+  // the cached policy.
   const int64_t kv_bytes = static_cast<int64_t>(B) * max_blocks * block_size * Hkv * D *
                            (dtype == TS_F32 ? 4 : 2) * 2;
-  const bool stream_kv = max_blocks > 0 && kv_bytes > (int64_t{256} << 20);
-  if (stream_kv && by_length) {
-    by_length = 0;
-    wpg = 1;
-  }
+  const bool stream_kv = max_blocks > 0 && (D == 64 || D == 128) && kv_bytes > (int64_t{256} << 20);
+  if (stream_kv && by_length) wpg = kMaxWavesLight;
   const bool light = stream_kv || light_budget(grid_waves, max_blocks > 0 && walk < 512);
   // With two waves per SIMD the chip holds twice the waves: up to 8 per workgroup, so
   // that each walks fewer tokens (fewer dependent rounds of loads per wave).
-  if (stream_kv) {
+  if (stream_kv && !by_length) {
     while (wpg < kMaxWavesLight && waves * wpg < 2 * want) wpg *= 2;
   } else if (light && !by_length) {
     while (wpg < kMaxWavesLight && waves * wpg * 2 <= 2 * want) wpg *= 2;
   }
+  plan->ht = ht;
+  plan->wpg = wpg;
+  plan->by_length = by_length;
+  plan->budget = !light ? kHeavy : stream_kv ? kLightStream : kLight;
+  plan->grid = dim3(Hq / ht, by_length ? (B + 1) / 2 : B, splits);
+  // LDS: one merged state per wave (two per wave for a pair); none for one-wave groups.
+  plan->lds = wpg > 1 ? static_cast<size_t>((by_length ? 2 : 1) * wpg * state_slot_bytes(ht, D)) : 0;
+  return 0;
+}
+
+}  // namespace ts
+
+extern "C" int ts_decode_plan(int B, int Hq, int Hkv, int D, int block_size, int max_blocks,
+                              int splits, int head_tile, int dtype, int* out) {
+  if (!out) return TS_EINVAL;
+  DecodePlan p;
+  const int rc = plan_decode(B, Hq, Hkv, D, block_size, max_blocks, splits, head_tile, dtype, &p);
+  if (rc) return rc;
+  out[0] = p.budget;
+  out[1] = p.wpg;
+  out[2] = p.by_length;
+  out[3] = p.ht;
+  out[4] = static_cast<int>(p.grid.x);
+  out[5] = static_cast<int>(p.grid.y);
+  out[6] = static_cast<int>(p.grid.z);
+  out[7] = static_cast<int>(p.lds);
+  return 0;
+}
+
+extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v_cache,
+                               const int32_t* block_tables, const int32_t* context_lens,
+                               void* out, float* m, float* l, float* acc, int B, int Hq,
+                               int Hkv, int D, int block_size, int64_t q_stride_b,
+                               int64_t q_stride_h, int64_t o_stride_b, int64_t o_stride_h,
+                               int64_t k_stride_slot, int64_t k_stride_head, int64_t bt_stride,
+                               int max_blocks, int splits, int head_tile, float scale, int dtype,
+                               void* stream) {
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || splits < 1 || !is_pow2(block_size))
+    return TS_EINVAL;
+  if (B == 0) return 0;
+  if (B > 65535) return TS_EUNSUPPORTED;  // sequences are the grid's y dimension
+  if (splits > 1 && (!m || !l || !acc)) return TS_EINVAL;
+  if (splits == 1 && !out) return TS_EINVAL;
+  DecodePlan p;
+  const int rc = plan_decode(B, Hq, Hkv, D, block_size, max_blocks, splits, head_tile, dtype, &p);
+  if (rc) return rc;
   AttendArgs a{q, k_cache, v_cache, block_tables, context_lens, out, m, l, acc, nullptr,
-               nullptr, Hq, group, ilog2(block_size), splits, wpg, 0, by_length, B, q_stride_b,
-               q_stride_h, o_stride_b, o_stride_h, k_stride_slot, k_stride_head, bt_stride,
-               scale * kLog2e, 0};
-  a.stream_kv = stream_kv ? 1 : 0;
-  dim3 grid(Hq / ht, by_length ? (B + 1) / 2 : B, splits);
-  return dispatch_attend<false>(a, dtype, D, ht, grid, light, static_cast<hipStream_t>(stream));
+               nullptr, Hq, Hq / Hkv, ilog2(block_size), splits, p.wpg, 0, p.by_length, B,
+               q_stride_b, q_stride_h, o_stride_b, o_stride_h, k_stride_slot, k_stride_head,
+               bt_stride, scale * kLog2e, 0};
+  a.stream_kv = p.budget == kLightStream ? 1 : 0;
+  return dispatch_attend<false>(a, dtype, D, p.ht, p.grid, p.budget != kHeavy, p.lds,
+                                static_cast<hipStream_t>(stream));
 }
 
 extern "C" int ts_decode_combine(const float* m, const float* l, const float* acc, void* out,

@@ -19,6 +19,8 @@ reference's does (:361-391).
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from tinyserve_amd import _lib
@@ -46,11 +48,11 @@ TARGET_PROGRAMS = 256
 NO_SPLIT_PROGRAMS = 256
 MAX_SPLITS = 16
 
-# Split counts up to this run as one launch: the kernel gives each (sequence, head tile) a
-# workgroup of up to 4 or 8 waves over contiguous block ranges, merged in LDS, so there
-# are no fp32 partials in HBM and no combine pass (at B=32 x 256 tokens, 4 splits: 10.0
-# us against 21.5 us for partials + combine). More splits write partials and combine
-# them.
+# Split counts from the policy up to this run as one launch: the kernel gives each
+# (sequence, head tile) a workgroup of up to 4 or 8 waves over contiguous block ranges,
+# merged in LDS, so there are no fp32 partials in HBM and no combine pass (at B=32 x 256
+# tokens: 10.0 us against 21.5 us for 4 partials + combine). More splits, and any count
+# a caller asks for, write partials and combine them.
 IN_GROUP_SPLITS = 4
 
 # Reference constants, kept for ``num_splits_for(..., target=..., no_split=...)`` callers
@@ -130,6 +132,23 @@ def num_splits_for(
     return max(1, min(want, MAX_SPLITS, max_blocks))
 
 
+BUDGETS = ("heavy", "light", "light_stream")
+
+
+def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
+                max_blocks: int, splits: int, head_tile: int = 0,
+                dtype: torch.dtype = torch.float16) -> dict[str, object]:  # fmt: skip
+    """How ``ts_decode_split`` runs a launch of these sizes (``splits`` as passed to it: 1
+    for the policy's in-workgroup split), without launching: the register budget, waves
+    per workgroup, whether workgroups take length pairs, query heads per wave, the grid
+    and the LDS per workgroup. The launch shape depends on sizes only."""
+    out = (ctypes.c_int32 * 8)()
+    _lib.call("ts_decode_plan", batch, num_q_heads, num_kv_heads, head_dim, block_size,
+              max_blocks, splits, head_tile, _lib.DTYPES[dtype], out)  # fmt: skip
+    return {"budget": BUDGETS[out[0]], "waves_per_group": out[1], "by_length": bool(out[2]),
+            "head_tile": out[3], "grid": (out[4], out[5], out[6]), "lds_bytes": out[7]}  # fmt: skip
+
+
 def _launch(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -180,19 +199,22 @@ def paged_decode_attention(
     scale: float,
     block_size: int,
 ) -> torch.Tensor:
-    """Decode attention for B sequences in one launch (triton_attention.py:330-358).
+    """Validated decode attention: one new query per sequence against its whole paged
+    context, B sequences per launch (triton_attention.py:330-358).
 
     Args:
-        q: ``[B, Hq, D]``, each sequence's one new query, RoPE-rotated.
-        k_cache, v_cache: ``[num_slots, Hkv, D]``, one layer of the cache, the new
-            tokens' k/v already written.
-        block_tables: ``[B, max_blocks]`` int32, each sequence's blocks in order.
-        context_lens: ``[B]`` int32, tokens per sequence including the new one (>= 1).
-        scale: multiplies the scores.
-        block_size: tokens per cache block.
+        q: ``[B, Hq, D]``, the rotated query of each sequence's newest token.
+        k_cache, v_cache: one layer's cache, ``[num_slots, Hkv, D]``, which must already
+            hold the newest tokens' keys and values.
+        block_tables: int32 ``[B, max_blocks]``; row b names sequence b's blocks in
+            order, and columns past its last block are ignored.
+        context_lens: int32 ``[B]``, each sequence's length counting the new token; at
+            least 1.
+        scale: factor applied to every q.k score.
+        block_size: slots per cache block.
 
     Returns:
-        ``[B, Hq, D]`` in q's dtype.
+        A new ``[B, Hq, D]`` tensor, q's dtype.
     """
     check_decode_args(q, k_cache, v_cache, block_tables, context_lens, block_size)
     return launch_paged_decode(q, k_cache, v_cache, block_tables, context_lens, scale, block_size)
@@ -278,15 +300,17 @@ def launch_paged_decode_split(
 ) -> torch.Tensor:
     """The split-K launches alone (:534-586): no checks, no host sync.
 
-    ``num_splits`` defaults to ``num_splits_for(B, Hkv, max_blocks)``. Up to
-    ``IN_GROUP_SPLITS`` the ranges are the waves of one workgroup, merged in LDS (one
-    launch; the library sizes the workgroup to the grid); more write fp32 partials that
-    a second launch combines."""
+    An explicit ``num_splits`` S > 1 runs as the reference runs it: S block ranges of
+    ``ceil(blocks / S)`` each write an fp32 partial (m, l, acc), and a second launch
+    combines them. Without one, the count comes from ``num_splits_for(B, Hkv,
+    max_blocks)``, and a policy count up to ``IN_GROUP_SPLITS`` becomes one launch
+    whose workgroups split each sequence over their waves and merge in LDS (the library
+    sizes the workgroup to the grid): no partials, no second launch."""
     b = q.shape[0]
     splits = num_splits or num_splits_for(b, k_cache.shape[1], block_tables.shape[1])
     if not 1 <= splits <= MAX_SPLITS:
         raise ValueError(f"num_splits must be 1..{MAX_SPLITS}, got {splits}")
     check_tile(tile or DECODE_TILE)
-    if splits <= IN_GROUP_SPLITS:
+    if num_splits is None and splits <= IN_GROUP_SPLITS:
         splits = 1
     return _launch(q, k_cache, v_cache, block_tables, context_lens, scale, block_size, splits, 0)

@@ -24,7 +24,8 @@ from tinyserve_amd import _lib
 
 
 def rms_norm_rows(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """``layers.rms_norm`` of every row of ``[T, N]`` in one launch (:116-126)."""
+    """RMSNorm (``layers.rms_norm``) applied to each of the T rows of ``x [T, N]``,
+    all rows in a single launch (:116-126)."""
     if x.dim() != 2 or x.stride(1) != 1 or weight.shape != (x.shape[1],):
         raise ValueError(f"need a row-contiguous [T, N] tensor and an [N] weight: {x.shape}")
     if weight.dtype != x.dtype or weight.stride(0) != 1:
@@ -51,19 +52,22 @@ def qk_norm_rope_store(
     v_cache: torch.Tensor,
     eps: float,
 ) -> torch.Tensor:
-    """q/k head norms, RoPE and the cache write of one layer, in one launch (:129-177).
+    """Per-head RMSNorm of q and k, rotary embedding of both, and the cache store of
+    this step's k and v, as a single launch for one layer (:129-177).
 
-    Returns ``apply_rope(rms_norm(q, q_weight, eps), cos, sin)`` and writes
-    ``apply_rope(rms_norm(k, k_weight, eps), cos, sin)`` and ``v`` to
-    ``k_cache[slots]`` / ``v_cache[slots]`` (cast to the cache dtype). No host sync.
+    The returned tensor is ``apply_rope(rms_norm(q, q_weight, eps), cos, sin)``. As a
+    side effect, row t of ``apply_rope(rms_norm(k, k_weight, eps), cos, sin)`` and of
+    ``v`` go to cache slot ``slots[t]`` of ``k_cache`` / ``v_cache``, converted to the
+    cache's dtype; no other slot is touched and the host never waits on the device.
 
     Args:
-        q: ``[T, Hq, D]``; k, v: ``[T, Hkv, D]``, head dimension contiguous (strided
-            views of a fused QKV projection are fine).
-        q_weight, k_weight: ``[D]``, q's dtype.
-        cos, sin: ``[T, D]`` float32 from ``rope_cos_sin`` (columns 0 .. D/2-1 are read).
-        slots: ``[T]`` int64 cache slots (int32 is widened).
-        k_cache, v_cache: ``[num_slots, Hkv, D]``, one layer.
+        q: ``[T, Hq, D]``; k, v: ``[T, Hkv, D]``. Only the head dimension must be
+            contiguous, so views into one fused QKV projection output work directly.
+        q_weight, k_weight: ``[D]`` in q's dtype.
+        cos, sin: float32 ``[T, D]`` tables from ``rope_cos_sin``; the kernel reads
+            their first D/2 columns.
+        slots: ``[T]`` int64 destination slots (int32 is accepted and widened).
+        k_cache, v_cache: ``[num_slots, Hkv, D]``, the layer's cache.
     """
     t, num_q_heads, head_dim = q.shape
     num_kv_heads = k.shape[1]

@@ -39,22 +39,28 @@ def paged_prefill_attention(
     num_warps: int | None = None,
     ieee: bool | None = None,
 ) -> torch.Tensor:
-    """Attention for R prefilling sequences in one launch, reading k/v from the cache.
+    """One launch of causal attention over a packed batch of R prompts (or prompt
+    chunks) whose keys and values are already in the paged cache
+    (triton_prefill.py:128-198).
 
-    Sequence r's queries are rows ``q_starts[r] .. q_starts[r] + q_lens[r] - 1`` of ``q``
-    and are its newest positions ``context_lens[r] - q_lens[r] ..``; each attends causally
-    to its own keys through ``block_tables[r]``.
+    Prompt r contributes ``q_lens[r]`` consecutive rows of ``q``, starting at row
+    ``q_starts[r]``; they are the last ``q_lens[r]`` of its ``context_lens[r]``
+    positions, and each row sees the positions up to and including its own, looked up
+    through ``block_tables[r]``.
 
     Args:
-        q: ``[T, Hq, D]`` RoPE-rotated queries; rows of other sequences are ignored.
-        k_cache, v_cache: ``[num_slots, Hkv, D]``, one layer, the new k/v already written.
-        block_tables: ``[R, max_blocks]`` int32.
-        q_starts, q_lens, context_lens: ``[R]`` int32.
-        max_q_len: the largest ``q_lens`` entry, from the host (sizes the grid, no sync).
-        out: ``[T, Hq, D]`` to write into (other rows are left alone); default
-            ``empty_like(q)``.
-        rows_per_tile, block_n, num_warps, ieee: the reference's Triton knobs; checked
-            like the reference (powers of 2, at least 16 rows / keys) and unused.
+        q: ``[T, Hq, D]`` queries after RoPE; rows no prompt claims are not read.
+        k_cache, v_cache: one layer of the cache, ``[num_slots, Hkv, D]``, already
+            holding this step's keys and values.
+        block_tables: int32 ``[R, max_blocks]``.
+        q_starts, q_lens, context_lens: int32 ``[R]``.
+        max_q_len: host-side maximum of ``q_lens``; it sizes the grid, so nothing is read
+            back from the device.
+        out: ``[T, Hq, D]`` receiving the claimed rows only (default: a new tensor like
+            ``q``).
+        rows_per_tile, block_n, num_warps, ieee: tuning knobs of the Triton kernel; they
+            are validated with the reference's rules and then ignored, since the HIP
+            kernel chooses its own tiles.
 
     Returns:
         ``out``.
