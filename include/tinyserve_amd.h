@@ -44,6 +44,7 @@ enum ts_dtype { TS_F32 = 0, TS_F16 = 1, TS_BF16 = 2 };
 /* Negative return codes (argument errors, detected before any launch). */
 #define TS_EINVAL (-1)      /* sizes or strides that do not fit together */
 #define TS_EUNSUPPORTED (-2) /* a shape/dtype combination with no compiled kernel */
+#define TS_ETOOBIG (-3)      /* ts_decode_attention_noalloc: partials beyond its scratch */
 
 /* Library version, (major << 16) | minor. */
 int ts_version(void);
@@ -99,6 +100,28 @@ int ts_decode_split(const void* q, const void* k_cache, const void* v_cache,
  */
 int ts_decode_plan(int B, int Hq, int Hkv, int D, int block_size, int max_blocks, int splits,
                    int head_tile, int dtype, int* plan);
+
+/*
+ * No counterpart in the reference. For callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * split-K decode of ts_decode_split + ts_decode_combine, with the fp32 split partials in
+ * a static device array of TS_NOALLOC_SCRATCH_BYTES per device instead of caller buffers.
+ * The caller passes inputs and `out` as for ts_decode_split (splits == 1 uses no
+ * scratch). Returns TS_ETOOBIG, before any launch, when B * Hq * splits * (D + 2) * 4
+ * bytes exceed the scratch. Allocates nothing (no hipMalloc, no library allocation); the
+ * first call on a device looks up that device's copy of the array, so call it with the
+ * stream's device current. Calls on one device share its array: calls that overlap in
+ * time on one device (different streams, different threads) race and must be serialised
+ * by the caller. Nothing needs clearing between calls: every partial is rewritten.
+ */
+#define TS_NOALLOC_SCRATCH_BYTES (16 << 20)
+int ts_decode_attention_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                const int32_t* block_tables, const int32_t* context_lens,
+                                void* out, int B, int Hq, int Hkv, int D, int block_size,
+                                int64_t q_stride_b, int64_t q_stride_h, int64_t o_stride_b,
+                                int64_t o_stride_h, int64_t k_stride_slot, int64_t k_stride_head,
+                                int64_t bt_stride, int max_blocks, int splits, int head_tile,
+                                float scale, int dtype, void* stream);
 
 /*
  * The split-K combine pass: out[b, h] = sum_s w_s acc_s / sum_s w_s l_s with

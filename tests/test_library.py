@@ -62,6 +62,11 @@ def test_c_abi_rejects_bad_sizes_before_any_launch(lib: ctypes.CDLL) -> None:
     assert lib.ts_prefill_varlen(*([null] * 8), 1, 12, 4, 32, 16, 4, 0, *strides, 1.0, 0, null) == -1
     assert lib.ts_rms_norm_rows(null, null, null, 4, 0, 0, 0, 1e-6, 0, null) == -1
     assert lib.ts_qk_norm_rope_store(*([null] * 11), 1, 4, 2, 12, *([0] * 11), 1e-6, 0, 0, null) == -1
+    # the no-allocation decode refuses partials beyond its scratch (2048 x 16 x 16 x 130
+    # floats > 16 MiB) before touching any pointer or device
+    assert lib.ts_decode_attention_noalloc(*([null] * 5), 1, 2048, 16, 8, 128, 16, *strides, 0, 16, 0,
+                                           1.0, 1, null) == -3  # fmt: skip
+    assert b"scratch" in lib.ts_strerror(-3)
     # empty batches launch nothing and succeed
     assert lib.ts_decode_split(*([null] * 9), 0, 4, 2, 32, 16, *strides, 0, 1, 0, 1.0, 0, null) == 0
     assert lib.ts_rms_norm_rows(null, null, null, 0, 16, 16, 16, 1e-6, 1, null) == 0

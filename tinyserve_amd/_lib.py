@@ -36,6 +36,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i, _i, _i, _f, _i, _vp],  # max_blocks splits head_tile scale dtype stream
     ),
     "ts_decode_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _i, _i, _c_i32p]),
+    "ts_decode_attention_noalloc": (
+        _i,
+        [_vp, _vp, _vp, _vp, _vp, _vp,  # q k v bt lens out
+         _i, _i, _i, _i, _i,  # B Hq Hkv D block_size
+         _i64, _i64, _i64, _i64, _i64, _i64, _i64,  # strides
+         _i, _i, _i, _f, _i, _vp],  # max_blocks splits head_tile scale dtype stream
+    ),
     "ts_decode_combine": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i64, _i64, _i, _i, _vp]),
     "ts_prefill_varlen": (
         _i,

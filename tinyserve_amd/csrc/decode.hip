@@ -36,6 +36,8 @@
 // cross-lane work except the LPT-lane dot-product reduction. The token lanes are
 // merged once at the end with the two-partial rule m = max(m1, m2),
 // l = 2^(m1-m) l1 + 2^(m2-m) l2 (same for acc), the rule the combine pass uses too.
+#include <mutex>
+
 #include "common.h"
 
 namespace ts {
@@ -830,12 +832,94 @@ extern "C" int ts_decode_combine(const float* m, const float* l, const float* ac
   }
 }
 
+// ---- the no-allocation variant ----------------------------------------------------------
+// The split partials of ts_decode_attention_noalloc live in this array: one copy per
+// device, held until the process ends. Host code never passes `scratch` itself (on the
+// host it names a stand-in, not device memory): the device address of each device's copy
+// is looked up once, with that device current, and kept.
+namespace ts {
+constexpr int64_t kNoAllocScratchFloats = TS_NOALLOC_SCRATCH_BYTES / sizeof(float);
+}  // namespace ts
+
+static __device__ __align__(256) float scratch[ts::kNoAllocScratchFloats];
+
+namespace ts {
+
+constexpr int kMaxScratchDevices = 64;
+static std::atomic<float*> g_scratch_ptr[kMaxScratchDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch array (hipGetSymbolAddress on the first
+// call per device). Returns 0 or a HIP error code.
+static int current_scratch(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return TS_EUNSUPPORTED;
+  float* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return e;
+      p = static_cast<float*>(addr);
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return 0;
+}
+
+}  // namespace ts
+
+extern "C" int ts_decode_attention_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                           const int32_t* block_tables, const int32_t* context_lens,
+                                           void* out, int B, int Hq, int Hkv, int D, int block_size,
+                                           int64_t q_stride_b, int64_t q_stride_h,
+                                           int64_t o_stride_b, int64_t o_stride_h,
+                                           int64_t k_stride_slot, int64_t k_stride_head,
+                                           int64_t bt_stride, int max_blocks, int splits,
+                                           int head_tile, float scale, int dtype, void* stream) {
+  if (B < 0 || Hq <= 0 || D <= 0 || splits < 1 || !out) return TS_EINVAL;
+  if (splits > 1) {
+    // acc [B, Hq, S, D] first (256-byte aligned, so its 16-byte stores stay aligned),
+    // then m and l [B, Hq, S].
+    const int64_t parts = static_cast<int64_t>(B) * Hq * splits;
+    if (parts * (D + 2) > kNoAllocScratchFloats) return TS_ETOOBIG;
+  }
+  if (B == 0) return 0;
+  if (splits == 1)
+    return ts_decode_split(q, k_cache, v_cache, block_tables, context_lens, out, nullptr, nullptr,
+                           nullptr, B, Hq, Hkv, D, block_size, q_stride_b, q_stride_h, o_stride_b,
+                           o_stride_h, k_stride_slot, k_stride_head, bt_stride, max_blocks, 1,
+                           head_tile, scale, dtype, stream);
+  float* base = nullptr;
+  const int rc = current_scratch(&base);
+  if (rc) return rc;
+  const int64_t parts = static_cast<int64_t>(B) * Hq * splits;
+  float* acc = base;
+  float* m = acc + parts * D;
+  float* l = m + parts;
+  // Every (sequence, head, split) partial is written by the split kernel (empty ranges as
+  // m = -inf, l = 0, acc = 0), so nothing left by an earlier call is read.
+  int e = ts_decode_split(q, k_cache, v_cache, block_tables, context_lens, out, m, l, acc, B, Hq,
+                          Hkv, D, block_size, q_stride_b, q_stride_h, o_stride_b, o_stride_h,
+                          k_stride_slot, k_stride_head, bt_stride, max_blocks, splits, head_tile,
+                          scale, dtype, stream);
+  if (e) return e;
+  return ts_decode_combine(m, l, acc, out, B, Hq, D, o_stride_b, o_stride_h, splits, dtype, stream);
+}
+
 extern "C" int ts_version(void) { return (0 << 16) | 1; }
 
 extern "C" const char* ts_strerror(int code) {
   if (code == 0) return "success";
   if (code == TS_EINVAL) return "invalid argument: sizes or strides do not fit together";
   if (code == TS_EUNSUPPORTED) return "unsupported shape or dtype: no compiled kernel";
+  if (code == TS_ETOOBIG)
+    return "the split partials exceed the no-allocation scratch (TS_NOALLOC_SCRATCH_BYTES per device)";
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
   return "unknown error";
 }

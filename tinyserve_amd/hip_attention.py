@@ -314,3 +314,38 @@ def launch_paged_decode_split(
     if num_splits is None and splits <= IN_GROUP_SPLITS:
         splits = 1
     return _launch(q, k_cache, v_cache, block_tables, context_lens, scale, block_size, splits, 0)
+
+
+def launch_paged_decode_split_noalloc(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    scale: float,
+    block_size: int,
+    out: torch.Tensor,
+    num_splits: int | None = None,
+) -> torch.Tensor:
+    """``launch_paged_decode_split`` into a caller-owned ``out``, with nothing allocated
+    on the device: the split partials go to the library's static per-device scratch
+    (``ts_decode_attention_noalloc``; no reference counterpart). For callers that cannot
+    allocate, such as code under graph capture. Split counts as in
+    ``launch_paged_decode_split``; a launch whose partials exceed the scratch raises
+    ValueError before anything runs. Calls that overlap in time on one device race."""
+    b, hq, d = q.shape
+    splits = num_splits or num_splits_for(b, k_cache.shape[1], block_tables.shape[1])
+    if not 1 <= splits <= MAX_SPLITS:
+        raise ValueError(f"num_splits must be 1..{MAX_SPLITS}, got {splits}")
+    if num_splits is None and splits <= IN_GROUP_SPLITS:
+        splits = 1
+    if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
+        raise ValueError(f"out must be like q {tuple(q.shape)} {q.dtype}")
+    dev = _lib.require_device(q, k_cache, v_cache, block_tables, context_lens, out)
+    _check_kernel_shape(q, k_cache)
+    _lib.call("ts_decode_attention_noalloc", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+              block_tables.data_ptr(), context_lens.data_ptr(), out.data_ptr(), b, hq,
+              k_cache.shape[1], d, block_size, q.stride(0), q.stride(1), out.stride(0), out.stride(1),
+              k_cache.stride(0), k_cache.stride(1), block_tables.stride(0), block_tables.shape[1],
+              splits, 0, scale, _lib.dtype_code(q), _lib.stream_of(dev))  # fmt: skip
+    return out
