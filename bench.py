@@ -387,7 +387,7 @@ def main() -> None:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--profile", choices=["prefill_varlen32", "fused_t4096"], default=None,
+    ap.add_argument("--profile", choices=["prefill_varlen32", "fused_t4096", "decode_b32_ctx256"], default=None,
                     help="only launch one workload 3 times (for a profiler) and print what ran")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run 3 plain device copies of this many MiB (a known-size kernel "
@@ -410,6 +410,15 @@ def main() -> None:
             paged_prefill_attention(*p.args(), out=out)
         torch.cuda.synchronize()
         print(json.dumps({"profile": args.profile, "launches": 3, "sequences": len(lens),
+                          **calibration_copies(args.copy_mb)}), flush=True)  # fmt: skip
+        return
+    if args.profile == "decode_b32_ctx256":  # config 2: 4 splits + combine, then the policy's launch
+        c = decode_bench_case(32, 256, pool_blocks=4096, device=torch.device("cuda:0"), seed=1)
+        for splits in (4, None):
+            for _ in range(20):
+                launch_paged_decode_split(*c.args(), c.scale, BS, num_splits=splits)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile": args.profile, "launches": "20 x (split kernel + combine), then 20 x one launch",
                           **calibration_copies(args.copy_mb)}), flush=True)  # fmt: skip
         return
     if args.profile == "fused_t4096":  # config 4's two fused kernels, eager, nothing else
