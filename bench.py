@@ -14,7 +14,7 @@ and lengths read: 1,074,332,160 B) divided by the measured time per step, in GB/
 restated) on the same workload on this host's cores. ``extra`` adds the prefill
 (MFMA-bound) and fused-kernel (HBM-bound) numbers of BASELINE configs 2-4.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--splits S] [--no-cpu] [--no-extra]
+    python bench.py [--gpus 1] [--steps 100] [--warmup 200] [--splits S] [--no-cpu] [--no-extra]
 """
 
 from __future__ import annotations
@@ -334,16 +334,20 @@ def extra_measurements() -> dict:
                           "qk_norm_rope_store": round(eager_q * 1e3, 2)}}  # fmt: skip
     # Config 5: the 28-layer decode step.
     res["decode_step_28l_b64"] = decode_step_28l()
+    res["decode_step_28l_b32_short_ctx_by_table_width"] = short_context_graph_widths()
     return res
 
 
-def decode_step_28l(batch: int = 64, steps: int = 20, seed: int = 5) -> dict:
+def decode_step_28l(batch: int = 64, steps: int = 20, seed: int = 5, ctx: tuple[int, int] = (1024, 4096),
+                    width: int | None = None, splits_list: tuple = (16, None)) -> dict:  # fmt: skip
     """one decode step of all 28 layers of a random-init
     Qwen3-0.6B-shaped model (fp16), B=64, contexts ~ U[1024, 4096], 16-token blocks
     scattered over the pool, replayed as a captured graph. Reported for the reference's
     16 splits and for this library's split policy: tokens/s and the decode-attention
     share of the step (a graph of the step's 28 attention launches alone, timed the
-    same way)."""
+    same way). ``width``: block-table columns of the step's buffers (default: the
+    longest sequence's blocks), e.g. the model's maximum position as a graph runner
+    sizes them."""
     from tinyserve_amd.decode_step import (DecodeGraph, DecodeStep, KVPool, ModelShape,
                                            random_context_tables, random_weights)  # fmt: skip
     from tinyserve_amd.step_inputs import DecodeInputs, PagedTable, fill_decode_inputs
@@ -352,36 +356,55 @@ def decode_step_28l(batch: int = 64, steps: int = 20, seed: int = 5) -> dict:
     shape = ModelShape()
     w = random_weights(shape, torch.float16, dev, seed)
     g = torch.Generator().manual_seed(seed)
-    lens = torch.randint(1024, 4097, (batch,), generator=g).tolist()
+    lens = torch.randint(ctx[0], ctx[1] + 1, (batch,), generator=g).tolist()
     blocks, nb = random_context_tables(lens, BS, seed=seed)
     pool = KVPool(shape, nb, BS, torch.float16, dev)
     gd = torch.Generator(device=dev).manual_seed(seed)
     pool.k.normal_(generator=gd)
     pool.v.normal_(generator=gd)
     tables = [PagedTable(b, BS, n) for b, n in zip(blocks, lens)]
-    inp = DecodeInputs.empty(batch, max(len(b) for b in blocks), dev)
+    inp = DecodeInputs.empty(batch, width or max(len(b) for b in blocks), dev)
     fill_decode_inputs(inp, [(i % shape.vocab, t) for i, t in enumerate(tables)], pool.pad_block)
     kv_bytes = sum(lens) * shape.num_layers * 2 * shape.kv_size * 2
-    res: dict = {"batch": batch, "ctx_mean": round(sum(lens) / batch, 1), "kv_read_GB": round(kv_bytes / 1e9, 2)}
-    for splits in (16, None):
+    res: dict = {"batch": batch, "ctx_mean": round(sum(lens) / batch, 1), "kv_read_GB": round(kv_bytes / 1e9, 2),
+                 "table_width": inp.block_tables.shape[1]}  # fmt: skip
+    for splits in splits_list:
         step = DecodeStep(shape, w, pool, splits)
         full = DecodeGraph(step.forward, inp)
         attn = DecodeGraph(step.attention_only, inp)
         ms_step = loop_ms(full.replay, steps, 3)
         ms_attn = loop_ms(attn.replay, steps, 3)
         used = splits or num_splits_for(batch, shape.num_kv_heads, inp.block_tables.shape[1])
+        plan = decode_plan(batch, HQ, HKV, D, BS, inp.block_tables.shape[1], 1 if splits is None and used <= 4 else used)
         res[f"splits_{used}"] = {"ms_per_step": round(ms_step, 3), "tok_per_s": round(batch / ms_step * 1e3, 1),
                                  "attention_ms": round(ms_attn, 3), "attention_share": round(ms_attn / ms_step, 3),
-                                 "attention_GB/s": round(kv_bytes / ms_attn / 1e6, 1)}  # fmt: skip
+                                 "attention_GB/s": round(kv_bytes / ms_attn / 1e6, 1),
+                                 "kernel": kernel_name(plan)}  # fmt: skip
         del full, attn
     return res
+
+
+def short_context_graph_widths(batch: int = 32) -> dict:
+    """The config-5 step at short contexts (B=32, contexts ~ U[192, 320]) through graph
+    buffers of two widths: the batch's own longest table, and the model's maximum
+    position (40,960 tokens: 2,560 blocks, as a graph runner sizes them). The wide table
+    bounds more than 256 MiB of K/V, so its launches stream K/V with non-temporal loads;
+    this measures what that costs inside a whole step."""
+    out = {}
+    for name, width in (("tight_table", None), ("max_position_table", 40960 // BS)):
+        out[name] = decode_step_28l(batch=batch, steps=20, seed=7, ctx=(192, 320), width=width,
+                                    splits_list=(None,))  # fmt: skip
+    return out
 
 
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    # The clocks ramp for the first few hundred back-to-back launches under sustained HBM
+    # load (~179 us per step over the first 50, ~164 us from the 150th on, one box): the
+    # untimed warmup covers the ramp, so the timed steps measure the steady state.
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--splits", type=int, default=0, help="0: the launcher's default policy")
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=4096)
