@@ -281,6 +281,14 @@ def extra_measurements() -> dict:
                     "launches": "split kernel + combine" if splits else "one launch",
                     "kernel": kernel_name(plan), "grid": plan["grid"],
                     "waves_per_group": plan["waves_per_group"]}  # fmt: skip
+    # The reference's own published decode shapes (fp16, one layer, Qwen3 heads; its T4
+    # timings in BASELINE.md): B=32 x 1024, B=32 x 160, B=64 x 1024, the policy's launch.
+    for b, ctx in ((32, 1024), (32, 160), (64, 1024)):
+        cr = decode_bench_case(b, ctx, device=dev, seed=2)
+        ms_r = graph_ms(lambda: launch_paged_decode_split(*cr.args(), cr.scale, BS))
+        nb_r = decode_bytes(b, ctx)["step"]
+        res[f"decode_b{b}_ctx{ctx}"] = {"us": round(ms_r * 1e3, 2), "GB/s": round(nb_r / ms_r / 1e6, 1),
+                                        "timing": "graph replay"}  # fmt: skip
     # Config 3: varlen prefill, 32 prompts L ~ U[16, 2048], fp16 and bf16.
     lens = prefill_lengths(32, seed=0)
     flops = sum(4 * HQ * D * n * (n + 1) // 2 for n in lens)
