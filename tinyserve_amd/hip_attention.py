@@ -311,7 +311,7 @@ def launch_paged_decode_split(
     if not 1 <= splits <= MAX_SPLITS:
         raise ValueError(f"num_splits must be 1..{MAX_SPLITS}, got {splits}")
     check_tile(tile or DECODE_TILE)
-    if num_splits is None and splits <= IN_GROUP_SPLITS:
+    if not num_splits and splits <= IN_GROUP_SPLITS:  # no count given (None or 0): the policy
         splits = 1
     return _launch(q, k_cache, v_cache, block_tables, context_lens, scale, block_size, splits, 0)
 
@@ -337,7 +337,7 @@ def launch_paged_decode_split_noalloc(
     splits = num_splits or num_splits_for(b, k_cache.shape[1], block_tables.shape[1])
     if not 1 <= splits <= MAX_SPLITS:
         raise ValueError(f"num_splits must be 1..{MAX_SPLITS}, got {splits}")
-    if num_splits is None and splits <= IN_GROUP_SPLITS:
+    if not num_splits and splits <= IN_GROUP_SPLITS:  # no count given (None or 0): the policy
         splits = 1
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
         raise ValueError(f"out must be like q {tuple(q.shape)} {q.dtype}")
