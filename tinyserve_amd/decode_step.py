@@ -155,11 +155,13 @@ class DecodeStep:
             w[p + "self_attn.k_norm.weight"], cos, sin, slots, self.pool.k[i],
             self.pool.v[i], s.rms_norm_eps)  # fmt: skip
         attn = attend(i, q)
-        # Residual adds ride in the GEMMs (beta = 1): one launch each instead of two.
-        x = torch.addmm(x, attn.reshape(n, s.q_size), w[p + "self_attn.o_proj.weight"].t())
+        # Residual adds ride in the GEMMs (beta = 1), in place: x is this step's own
+        # activation, and an out-of-place addmm would first copy x into a new output (one
+        # more launch per add).
+        x.addmm_(attn.reshape(n, s.q_size), w[p + "self_attn.o_proj.weight"].t())
         h = hip_fused.rms_norm_rows(x, w[p + "post_attention_layernorm.weight"], s.rms_norm_eps)
         gate, up = F.linear(h, w[p + "mlp.gate_up_proj.weight"]).chunk(2, dim=1)
-        return torch.addmm(x, F.silu(gate) * up, w[p + "mlp.down_proj.weight"].t())
+        return x.addmm_(F.silu(gate) * up, w[p + "mlp.down_proj.weight"].t())
 
     def _run(self, token_ids: torch.Tensor, positions: torch.Tensor, slots: torch.Tensor,
              attend: Callable[[int, torch.Tensor], torch.Tensor],
