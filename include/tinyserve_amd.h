@@ -186,6 +186,54 @@ int ts_qk_norm_rope_store(const void* q, const void* k, const void* v, void* q_o
                           int64_t c_stride_head, float eps, int dtype, int cache_dtype,
                           void* stream);
 
+/*
+ * Projections of a decode step: out = x . W^T for M rows (a few per sequence) against a
+ * weight matrix W [N, K] (row stride w_stride) streamed once. No counterpart in the
+ * reference's kernels: these replace the F.linear calls of the decoder layer and the
+ * residual adds around them (model.py:137-179) on the decode path; x, W and the outputs
+ * share `dtype` (fp16 or bf16). `epilogue`:
+ *   TS_ROWS_STORE (0):   out [M, N] (row stride o_stride) = (dtype)(x . W^T)
+ *   TS_ROWS_PARTIAL (1): partial [KS][M][N] fp32 = partial sums over KS slices of K, to be
+ *                        added by ts_add_rms_norm (KS from ts_rows_gemm_plan; partial
+ *                        holds partial_floats floats, at least KS * M * N)
+ *   TS_ROWS_SILU (2):    W = [gate; up] (2N rows); out = (dtype)(silu(gate) * up), each
+ *                        factor rounded as F.silu / F.linear round it, written
+ *                        operand-tiled [Mpad, N] (N % 32 == 0)
+ * x_tiled: x is operand-tiled [Mpad, K] (as TS_ROWS_SILU and ts_add_rms_norm write it),
+ * else row-major with row stride x_stride. Operand-tiled layout, Mpad = M rounded up to
+ * 64: element (m, k) sits at
+ *   ((((m/64) * (K/32) + k/32) * 4 + (m%64)/16) * 64 + ((k%32)/8) * 16 + m%16) * 8 + k%8.
+ * Pointers 16-byte aligned, strides multiples of 8 elements.
+ */
+#define TS_ROWS_STORE 0
+#define TS_ROWS_PARTIAL 1
+#define TS_ROWS_SILU 2
+int ts_rows_gemm(const void* x, int x_tiled, int64_t x_stride, const void* w, int64_t w_stride,
+                 void* out, int64_t o_stride, float* partial, int64_t partial_floats, int M, int N,
+                 int K, int epilogue, int dtype, void* stream);
+
+/*
+ * The launch shape ts_rows_gemm picks: out[0] waves per workgroup, out[1] 16-row tiles
+ * of W per wave, out[2] 32-column steps per wave, out[3] KS (workgroups along K),
+ * out[4] chunks each workgroup walks. No counterpart in the reference.
+ */
+int ts_rows_gemm_plan(int M, int N, int K, int epilogue, int* out);
+
+/*
+ * The residual add + RMSNorm between two projections of a decode step (model.py:170-177:
+ * x = x + F.linear(...); h = rms_norm(x)). No counterpart in the reference's kernels.
+ *   ks > 0:  x_out = (dtype)(x + partial[0] + ... + partial[ks-1])  (partial [ks][M][N]
+ *            fp32 from ts_rows_gemm TS_ROWS_PARTIAL; x_out may be x itself)
+ *   ks == 0: the residual is x unchanged (x_out is not written)
+ *   h = the RMSNorm of that residual times w, rounded as ts_rms_norm_rows rounds it,
+ *       row-major (row stride h_stride) or operand-tiled [Mpad, N] (h_tiled, N % 32 == 0;
+ *       padding rows written as zeros).
+ * N <= 4096 and a multiple of 8.
+ */
+int ts_add_rms_norm(const void* x, int64_t x_stride, const float* partial, int ks, const void* w,
+                    void* x_out, int64_t xo_stride, void* h, int h_tiled, int64_t h_stride, int M,
+                    int N, float eps, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -211,12 +211,13 @@ CONFIG5 = ModelShape()  # Qwen3-0.6B: hidden 1024, 16/8 heads of 128, inter 3072
 CHECKED_LAYERS = (0, 13, 27)
 
 
-@pytest.mark.parametrize("splits", [16, None])
-def test_config_5_step_at_full_shape(splits: int | None, monkeypatch: pytest.MonkeyPatch) -> None:
+@pytest.mark.parametrize(("splits", "projections"), [(16, "rows"), (None, "rows"), (None, "library")])
+def test_config_5_step_at_full_shape(splits: int | None, projections: str, monkeypatch: pytest.MonkeyPatch) -> None:
     # BASELINE config 5 at its real shape, as bench.py runs it: the random-init
     # Qwen3-0.6B-shaped model in fp16, B=64, contexts ~ U[1024, 4096], 16-token blocks
     # scattered over the pool; the reference's 16 splits (HBM partials + combine) and
-    # this library's policy. Layers 0, 13 and 27: the fused kernel's q and cache writes
+    # this library's policy; the projections on the row-batch kernels (the default) and
+    # on library GEMMs. Layers 0, 13 and 27: the fused kernel's q and cache writes
     # and the attention output against the oracle on the same fp16 inputs, at the
     # contract's bounds. Then the logits of the whole 28-layer step against the
     # oracle-composed step in float32 (run on the GPU as the checker).
@@ -252,7 +253,9 @@ def test_config_5_step_at_full_shape(splits: int | None, monkeypatch: pytest.Mon
 
     monkeypatch.setattr(hip_fused, "qk_norm_rope_store", qk)
     monkeypatch.setattr(hip_attention, "launch_paged_decode_split", attn)
-    logits = DecodeStep(s, w, pool, splits).forward(inp)
+    step = DecodeStep(s, w, pool, splits, projections)
+    assert step.projections == projections
+    logits = step.forward(inp)
     torch.cuda.synchronize()
     assert len(seen["qk"]) == len(seen["attn"]) == s.num_layers
     new = inp.slots[:batch]
@@ -277,6 +280,41 @@ def test_config_5_step_at_full_shape(splits: int | None, monkeypatch: pytest.Mon
     want_logits = reference_step(s, w, k32, v32, inp, bs, device=DEVICE)
     err = (logits.float() - want_logits).abs().max().item()
     scale = want_logits.abs().max().item()
-    print(f"[config 5] splits={splits}: logits max-abs {err:.3g} (max |logit| {scale:.3g})")
+    print(f"[config 5] splits={splits} {projections}: logits max-abs {err:.3g} (max |logit| {scale:.3g})")
     # fp16 activations over 28 layers against an all-fp32 composition: stated bound.
     torch.testing.assert_close(logits.float(), want_logits, atol=LOGITS_ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows", [5, 8])
+def test_row_projections_match_the_reference_step(dtype: torch.dtype, rows: int) -> None:
+    # The tiny model in 16-bit types through both projection paths: each against the
+    # oracle-composed fp32 step, and the two against each other (same kernels elsewhere).
+    lens = [9, 30, 2, 17, 5]
+    outs = {}
+    for projections in ("rows", "library"):
+        w, pool, tabs, inp = setup(lens, rows, dtype, seed=13)
+        kr, vr = pool.k.float().cpu(), pool.v.float().cpu()
+        want = reference_step(TINY, w, kr, vr, inp, pool.block_size)[: len(lens)]
+        step = DecodeStep(TINY, w, pool, None, projections)
+        assert step.projections == projections
+        outs[projections] = step.forward(inp)[: len(lens)].cpu()
+        err = (outs[projections] - want).abs().max().item()
+        print(f"[tiny {dtype}] {projections}: logits max-abs {err:.3g} vs fp32")
+        torch.testing.assert_close(outs[projections], want, atol=0.05 if dtype == torch.float16 else 0.2, rtol=0)
+        # The new tokens' k/v went to the cache (the v copy through the fused kernel).
+        real = inp.slots.cpu()[: len(lens)]
+        torch.testing.assert_close(pool.v.float().cpu()[:, real], vr[:, real],
+                                   atol=2e-3 if dtype == torch.float16 else 2e-2, rtol=2e-2)  # fmt: skip
+    torch.testing.assert_close(outs["rows"], outs["library"], atol=0.05 if dtype == torch.float16 else 0.2, rtol=0)
+
+
+def test_projection_choice() -> None:
+    w, pool, _, _ = setup([3], 1, torch.float32)
+    assert DecodeStep(TINY, w, pool).projections == "library"  # fp32: no MFMA projection kernels
+    with pytest.raises(ValueError, match="row-batch"):
+        DecodeStep(TINY, w, pool, projections="rows")
+    with pytest.raises(ValueError, match="projections"):
+        DecodeStep(TINY, w, pool, projections="fast")
+    w16, pool16, _, _ = setup([3], 1, torch.float16)
+    assert DecodeStep(TINY, w16, pool16).projections == "rows"

@@ -90,6 +90,14 @@ __device__ __forceinline__ float halves_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// RMSNorm's output element: y = (T)(x * r) * w, the multiply by w in T's precision (exact
+// product, one rounding), as layers.py:14-38 computes it in the model dtype.
+template <typename T>
+__device__ __forceinline__ T norm_scale(T x, float r, T w) {
+  const T xn = from_f32<T>(to_f32(x) * r);
+  return from_f32<T>(to_f32(xn) * to_f32(w));
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 inline int ilog2(int x) {

@@ -40,13 +40,6 @@ struct Chunk {
   }
 };
 
-// y = (T)(x * r) * w, the multiply by w in T's precision (exact product, one rounding).
-template <typename T>
-__device__ __forceinline__ T norm_scale(T x, float r, T w) {
-  const T xn = from_f32<T>(to_f32(x) * r);
-  return from_f32<T>(to_f32(xn) * to_f32(w));
-}
-
 // ---------------------------------------------------------------------------------
 // rms_norm_rows: one wave per row; lane l holds chunks l, l + 64, ... of VEC elements.
 // CPL = chunks per lane held in registers (N <= CPL * 64 * VEC).

@@ -3,19 +3,25 @@ reference's ``Qwen3.forward_decode`` with its fused kernels and a kernel decode
 (src/tinyserve/model.py:137-179, 332-356), and a captured graph of it like the
 reference's ``DecodeGraphs`` (src/tinyserve/cuda_graphs.py:135-173).
 
-Per layer, on the flat ``[N]`` rows of a ``DecodeInputs`` (step_inputs.py):
+Per layer, on the flat ``[N]`` rows of a ``DecodeInputs`` (step_inputs.py), with the
+projections on the row-batch kernels (hip_rows.py; fp16/bf16, up to 256 rows):
 
-    h    = rms_norm_rows(x, input_layernorm)                       HIP  (fused.hip)
-    qkv  = h @ W_qkv^T                                             GEMM (hipBLASLt via torch)
-    q    = qk_norm_rope_store(q, k, v, ...) -> K/V cache at slots  HIP  (fused.hip)
-    attn = paged decode attention over the block tables            HIP  (decode.hip)
-    x   += attn @ W_o^T                                             GEMM, residual add in it
-    h    = rms_norm_rows(x, post_attention_layernorm)              HIP
-    x   += (silu(gate) * up) @ W_down^T, [gate | up] = h @ W_gate_up^T
+    h    = add_rms_norm(x += previous layer's down partials, input_layernorm)  HIP (rows.hip)
+    qkv  = rows_linear(h, W_qkv)                                              HIP (rows.hip)
+    q    = qk_norm_rope_store(q, k, v, ...) -> K/V cache at slots             HIP (fused.hip)
+    attn = paged decode attention over the block tables                       HIP (decode.hip)
+    part = rows_linear_partials(attn, W_o)                                    HIP (rows.hip)
+    h    = add_rms_norm(x += part, post_attention_layernorm)                  HIP
+    act  = rows_silu_gate_up(h, W_gate_up)      (silu(gate) * up)             HIP
+    part = rows_linear_partials(act, W_down)    (added by the next add_rms_norm)
 
-then the final norm and the tied output head (``[vocab, hidden]``), padded to 8 rows as
-the reference pads it (model.py:214-221). The GEMMs and the SiLU product are library
-work outside the attention hot path; everything on the path is a HIP kernel.
+then the final norm (adding the last layer's down partials) and the tied output head
+(``[vocab, hidden]``, a library GEMM), padded to 8 rows as the reference pads it
+(model.py:214-221). Other dtypes and larger row counts (a mixed prefill step) take the
+projections through library GEMMs instead:
+
+    h = rms_norm_rows(x); qkv = h @ W_qkv^T; ...; x += attn @ W_o^T (addmm, in place);
+    h = rms_norm_rows(x); x += (silu(gate) * up) @ W_down^T
 
 Weights are random (no checkpoints here): linear weights ~ N(0, 0.02) in the model dtype,
 norm weights 1 + 0.1 N(0, 1). The KV pool has the reference's layout (kv_cache.py:20-50):
@@ -33,10 +39,11 @@ import torch.nn.functional as F
 
 from collections.abc import Callable
 
-from tinyserve_amd import hip_attention, hip_fused, hip_prefill
+from tinyserve_amd import hip_attention, hip_fused, hip_prefill, hip_rows
 from tinyserve_amd.step_inputs import Batch, DecodeInputs
 
 HEAD_MIN_ROWS = 8  # the output head runs on at least this many rows (model.py:64)
+ROWS_MAX = 256  # steps of more rows take the projections through library GEMMs
 
 
 @dataclass(frozen=True)
@@ -125,15 +132,26 @@ class DecodeStep:
     so a graph can capture it.
 
     ``num_splits``: the decode kernel's split count (None: the launcher's policy; the
-    reference's config-5 step forces 16)."""
+    reference's config-5 step forces 16). ``projections``: "rows" (the row-batch HIP
+    kernels), "library" (library GEMMs) or "auto" (rows where the dtype and shapes allow,
+    for steps of up to ``ROWS_MAX`` rows)."""
 
     def __init__(self, shape: ModelShape, weights: dict[str, torch.Tensor], pool: KVPool,
-                 num_splits: int | None = None) -> None:  # fmt: skip
+                 num_splits: int | None = None, projections: str = "auto") -> None:  # fmt: skip
         self.shape = shape
         self.w = weights
         self.pool = pool
         self.num_splits = num_splits
         self.scale = shape.head_dim**-0.5
+        dtype = weights["model.embed_tokens.weight"].dtype
+        fits = (hip_rows.supported(dtype) and shape.hidden % 32 == 0 and shape.intermediate % 32 == 0
+                and shape.q_size % 32 == 0 and shape.hidden <= 4096)  # fmt: skip
+        if projections not in ("auto", "rows", "library"):
+            raise ValueError(f"projections must be 'auto', 'rows' or 'library', got {projections!r}")
+        if projections == "rows" and not fits:
+            raise ValueError(f"the row-batch projections need fp16/bf16 and 32-aligned widths (hidden <= 4096), "
+                             f"got {dtype} and {shape}")  # fmt: skip
+        self.projections = projections if projections != "auto" else ("rows" if fits else "library")
 
     def _attention(self, i: int, q: torch.Tensor, inputs: DecodeInputs) -> torch.Tensor:
         return hip_attention.launch_paged_decode_split(
@@ -163,6 +181,32 @@ class DecodeStep:
         gate, up = F.linear(h, w[p + "mlp.gate_up_proj.weight"]).chunk(2, dim=1)
         return x.addmm_(F.silu(gate) * up, w[p + "mlp.down_proj.weight"].t())
 
+    def _layers_rows(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, slots: torch.Tensor,
+                     attend: Callable[[int, torch.Tensor], torch.Tensor]) -> torch.Tensor:  # fmt: skip
+        """Every layer and the final norm with the row-batch projection kernels: returns
+        the final-normed rows. ``x`` (this step's embedded rows) is updated in place: each
+        residual add happens in the ``add_rms_norm`` that follows it."""
+        s, w = self.shape, self.w
+        n = x.shape[0]
+        eps = s.rms_norm_eps
+        pending = None  # the previous layer's down_proj partials, not yet added to x
+        for i in range(s.num_layers):
+            p = f"model.layers.{i}."
+            h = hip_rows.add_rms_norm(x, pending, w[p + "input_layernorm.weight"], eps)
+            qkv = hip_rows.rows_linear(h, w[p + "self_attn.qkv_proj.weight"])
+            q, k, v = torch.split(qkv, [s.q_size, s.kv_size, s.kv_size], dim=1)
+            q = hip_fused.qk_norm_rope_store(
+                q.view(n, s.num_heads, s.head_dim), k.view(n, s.num_kv_heads, s.head_dim),
+                v.view(n, s.num_kv_heads, s.head_dim), w[p + "self_attn.q_norm.weight"],
+                w[p + "self_attn.k_norm.weight"], cos, sin, slots, self.pool.k[i],
+                self.pool.v[i], eps)  # fmt: skip
+            attn = attend(i, q)
+            part, _ = hip_rows.rows_linear_partials(attn.reshape(n, s.q_size), w[p + "self_attn.o_proj.weight"])
+            h = hip_rows.add_rms_norm(x, part, w[p + "post_attention_layernorm.weight"], eps)
+            act = hip_rows.rows_silu_gate_up(h, w[p + "mlp.gate_up_proj.weight"])
+            pending, _ = hip_rows.rows_linear_partials(act, w[p + "mlp.down_proj.weight"])
+        return hip_rows.add_rms_norm(x, pending, w["model.norm.weight"], eps, tiled=False)
+
     def _run(self, token_ids: torch.Tensor, positions: torch.Tensor, slots: torch.Tensor,
              attend: Callable[[int, torch.Tensor], torch.Tensor],
              rows: torch.Tensor | None = None) -> torch.Tensor:  # fmt: skip
@@ -170,11 +214,14 @@ class DecodeStep:
         s = self.shape
         cos, sin = rope_tables(s.head_dim, s.rope_theta, positions)
         x = self.w["model.embed_tokens.weight"][token_ids]
-        for i in range(s.num_layers):
-            x = self.layer(i, x, cos, sin, slots, attend)
+        if self.projections == "rows" and x.shape[0] <= ROWS_MAX:
+            x = self._layers_rows(x, cos, sin, slots, attend)
+        else:
+            for i in range(s.num_layers):
+                x = self.layer(i, x, cos, sin, slots, attend)
+            x = hip_fused.rms_norm_rows(x, self.w["model.norm.weight"], s.rms_norm_eps)
         if rows is not None:
             x = x[rows]
-        x = hip_fused.rms_norm_rows(x, self.w["model.norm.weight"], s.rms_norm_eps)
         n = x.shape[0]
         if n < HEAD_MIN_ROWS:
             x = F.pad(x, (0, 0, 0, HEAD_MIN_ROWS - n))
