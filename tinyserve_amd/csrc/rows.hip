@@ -173,40 +173,38 @@ __global__ __launch_bounds__(KP * kWave) void rows_gemm_kernel(const RowsArgs a)
     return v;
   };
 
-  if constexpr (KP > 1) {
+  if constexpr (KP > 1 && EPI == kSiluGateUp) {
+    // One output element per thread at a time (consecutive threads, consecutive
+    // columns): the SiLU's exp and roundings are spread over every thread. Rows past M
+    // are written as zeros: the tiled output is read whole.
+    for (int u = tid; u < kRowBlock * 16; u += KP * kWave) {
+      const int m = u / 16, j = u % 16;
+      const int row = mb * kRowBlock + m;
+      float v = 0.f;
+      if (row < a.M) {
+        const float g = to_f32(from_f32<T>(total(m, j)));
+        const float up = to_f32(from_f32<T>(total(m, 16 + j)));
+        v = to_f32(from_f32<T>(g / (1.0f + expf(-g)))) * up;
+      }
+      static_cast<T*>(a.out)[tiled_index(row, n0 + j, a.N)] = from_f32<T>(v);
+    }
+  } else if constexpr (KP > 1) {
     // Thread u handles 8 consecutive columns of one row: 16-byte stores.
-    constexpr int GROUPS = (EPI == kSiluGateUp ? 16 : BN) / 8;
+    constexpr int GROUPS = BN / 8;
     for (int u = tid; u < kRowBlock * GROUPS; u += KP * kWave) {
       const int m = u / GROUPS, j0 = (u % GROUPS) * 8;
       const int row = mb * kRowBlock + m;
-      if constexpr (EPI == kSiluGateUp) {
-        // Rows past M are written as zeros: the tiled output is read whole.
+      if (row >= a.M) continue;
+      if constexpr (EPI == kStore) {
         Pack16<T> y;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float v = 0.f;
-          if (row < a.M) {
-            const float g = to_f32(from_f32<T>(total(m, j0 + e)));
-            const float up = to_f32(from_f32<T>(total(m, 16 + j0 + e)));
-            const float s = to_f32(from_f32<T>(g / (1.0f + expf(-g))));
-            v = s * up;
-          }
-          y.v[e] = from_f32<T>(v);
-        }
-        store16(static_cast<T*>(a.out) + tiled_index(row, n0 + j0, a.N), y);
+        for (int e = 0; e < 8; ++e) y.v[e] = from_f32<T>(total(m, j0 + e));
+        store16(static_cast<T*>(a.out) + row * a.os + n0 + j0, y);
       } else {
-        if (row >= a.M) continue;
-        if constexpr (EPI == kStore) {
-          Pack16<T> y;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) y.v[e] = from_f32<T>(total(m, j0 + e));
-          store16(static_cast<T*>(a.out) + row * a.os + n0 + j0, y);
-        } else {
-          float* p = a.partial + (static_cast<int64_t>(blockIdx.z) * a.M + row) * a.N + n0 + j0;
-          *reinterpret_cast<r_f32x4*>(p) = r_f32x4{total(m, j0), total(m, j0 + 1), total(m, j0 + 2), total(m, j0 + 3)};
-          *reinterpret_cast<r_f32x4*>(p + 4) =
-              r_f32x4{total(m, j0 + 4), total(m, j0 + 5), total(m, j0 + 6), total(m, j0 + 7)};
-        }
+        float* p = a.partial + (static_cast<int64_t>(blockIdx.z) * a.M + row) * a.N + n0 + j0;
+        *reinterpret_cast<r_f32x4*>(p) = r_f32x4{total(m, j0), total(m, j0 + 1), total(m, j0 + 2), total(m, j0 + 3)};
+        *reinterpret_cast<r_f32x4*>(p + 4) =
+            r_f32x4{total(m, j0 + 4), total(m, j0 + 5), total(m, j0 + 6), total(m, j0 + 7)};
       }
     }
   } else {
@@ -361,24 +359,52 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(const T* __restrict__
     }
   }
   if (ks > 0) {
-    // The residual stream: x + (sum of the projection's partials), rounded once.
+    // The residual stream: x + (sum of the projection's partials in z order), rounded
+    // once. The partials are loaded ZG at a time, every load of a group issued before the
+    // first add (ZG * CPL * 8 floats of registers): one round trip per group instead of
+    // one per partial.
+    constexpr int ZG = 16 / CPL > 0 ? 16 / CPL : 1;
+    float s[CPL][8];
+#pragma unroll
+    for (int k = 0; k < CPL; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s[k][e] = 0.f;
+    for (int z0 = 0; z0 < ks; z0 += ZG) {
+      r_f32x4 pv[ZG][CPL][2];
+#pragma unroll
+      for (int z = 0; z < ZG; ++z) {
+        if (z0 + z < ks) {
+#pragma unroll
+          for (int k = 0; k < CPL; ++k) {
+            const int i = (k * kWave + lane) * 8;
+            if (i < N) {
+              const float* p = part + (static_cast<int64_t>(z0 + z) * M + row) * N + i;
+              pv[z][k][0] = *reinterpret_cast<const r_f32x4*>(p);
+              pv[z][k][1] = *reinterpret_cast<const r_f32x4*>(p + 4);
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int z = 0; z < ZG; ++z) {
+        if (z0 + z < ks) {
+#pragma unroll
+          for (int k = 0; k < CPL; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              s[k][e] += pv[z][k][0][e];
+              s[k][4 + e] += pv[z][k][1][e];
+            }
+        }
+      }
+    }
 #pragma unroll
     for (int k = 0; k < CPL; ++k) {
       const int i = (k * kWave + lane) * 8;
       if (i >= N) continue;
-      float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int z = 0; z < ks; ++z) {
-        const float* p = part + (static_cast<int64_t>(z) * M + row) * N + i;
-        const r_f32x4 lo = *reinterpret_cast<const r_f32x4*>(p);
-        const r_f32x4 hi = *reinterpret_cast<const r_f32x4*>(p + 4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s[e] += lo[e];
-          s[4 + e] += hi[e];
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xv[k].v[e] = from_f32<T>(s[e] + to_f32(xv[k].v[e]));
+      for (int e = 0; e < 8; ++e) xv[k].v[e] = from_f32<T>(s[k][e] + to_f32(xv[k].v[e]));
       store16(xo + row * xos + i, xv[k]);
     }
   }
