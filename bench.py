@@ -347,7 +347,8 @@ def extra_measurements() -> dict:
 
 
 def decode_step_28l(batch: int = 64, steps: int = 20, seed: int = 5, ctx: tuple[int, int] = (1024, 4096),
-                    width: int | None = None, splits_list: tuple = (16, None)) -> dict:  # fmt: skip
+                    width: int | None = None,
+                    variants: tuple = ((16, "rows"), (None, "rows"), (None, "library"))) -> dict:  # fmt: skip
     """one decode step of all 28 layers of a random-init
     Qwen3-0.6B-shaped model (fp16), B=64, contexts ~ U[1024, 4096], 16-token blocks
     scattered over the pool, replayed as a captured graph. Reported for the reference's
@@ -355,7 +356,9 @@ def decode_step_28l(batch: int = 64, steps: int = 20, seed: int = 5, ctx: tuple[
     share of the step (a graph of the step's 28 attention launches alone, timed the
     same way). ``width``: block-table columns of the step's buffers (default: the
     longest sequence's blocks), e.g. the model's maximum position as a graph runner
-    sizes them."""
+    sizes them. ``variants``: (split count, projections) pairs; "rows" runs the
+    projections on this library's row-batch kernels, "library" on library GEMMs (keys
+    ``splits_<S>`` and ``splits_<S>_library_projections``)."""
     from tinyserve_amd.decode_step import (DecodeGraph, DecodeStep, KVPool, ModelShape,
                                            random_context_tables, random_weights)  # fmt: skip
     from tinyserve_amd.step_inputs import DecodeInputs, PagedTable, fill_decode_inputs
@@ -376,18 +379,19 @@ def decode_step_28l(batch: int = 64, steps: int = 20, seed: int = 5, ctx: tuple[
     kv_bytes = sum(lens) * shape.num_layers * 2 * shape.kv_size * 2
     res: dict = {"batch": batch, "ctx_mean": round(sum(lens) / batch, 1), "kv_read_GB": round(kv_bytes / 1e9, 2),
                  "table_width": inp.block_tables.shape[1]}  # fmt: skip
-    for splits in splits_list:
-        step = DecodeStep(shape, w, pool, splits)
+    for splits, projections in variants:
+        step = DecodeStep(shape, w, pool, splits, projections)
         full = DecodeGraph(step.forward, inp)
         attn = DecodeGraph(step.attention_only, inp)
         ms_step = loop_ms(full.replay, steps, 3)
         ms_attn = loop_ms(attn.replay, steps, 3)
         used = splits or num_splits_for(batch, shape.num_kv_heads, inp.block_tables.shape[1])
         plan = decode_plan(batch, HQ, HKV, D, BS, inp.block_tables.shape[1], 1 if splits is None and used <= 4 else used)
-        res[f"splits_{used}"] = {"ms_per_step": round(ms_step, 3), "tok_per_s": round(batch / ms_step * 1e3, 1),
+        key = f"splits_{used}" + ("" if projections == "rows" else f"_{projections}_projections")
+        res[key] = {"ms_per_step": round(ms_step, 3), "tok_per_s": round(batch / ms_step * 1e3, 1),
                                  "attention_ms": round(ms_attn, 3), "attention_share": round(ms_attn / ms_step, 3),
                                  "attention_GB/s": round(kv_bytes / ms_attn / 1e6, 1),
-                                 "kernel": kernel_name(plan)}  # fmt: skip
+                                 "kernel": kernel_name(plan), "projections": projections}  # fmt: skip
         del full, attn
     return res
 
@@ -401,7 +405,7 @@ def short_context_graph_widths(batch: int = 32) -> dict:
     out = {}
     for name, width in (("tight_table", None), ("max_position_table", 40960 // BS)):
         out[name] = decode_step_28l(batch=batch, steps=20, seed=7, ctx=(192, 320), width=width,
-                                    splits_list=(None,))  # fmt: skip
+                                    variants=((None, "rows"),))  # fmt: skip
     return out
 
 
