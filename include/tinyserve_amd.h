@@ -166,6 +166,15 @@ int ts_rms_norm_rows(const void* x, const void* w, void* out, int T, int N,
                      int64_t x_stride, int64_t o_stride, float eps, int dtype, void* stream);
 
 /*
+ * The RoPE tables of T positions (int64): cos / sin [T, D] float32 (row stride `stride`),
+ * laid out as cat([angles, angles], -1) with angles[t, i] = positions[t] * theta^(-2i/D)
+ * computed in float64. Replaces rope_cos_sin (layers.py:41-65), which the reference's
+ * model evaluates with PyTorch ops once per step.
+ */
+int ts_rope_cos_sin(const int64_t* positions, int T, int D, double theta, float* cos_out,
+                    float* sin_out, int64_t stride, void* stream);
+
+/*
  * Per-head RMSNorm + rotate-half RoPE of q and k, and the paged KV-cache write.
  * Replaces _qk_norm_rope_store_kernel / qk_norm_rope_store (triton_fused.py:43-113,
  * :129-177).

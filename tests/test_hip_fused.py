@@ -14,7 +14,7 @@ import torch
 
 from oracle import ref
 from tests.helpers import ULP, assert_contract, assert_matches
-from tinyserve_amd.hip_fused import qk_norm_rope_store, rms_norm_rows
+from tinyserve_amd.hip_fused import qk_norm_rope_store, rms_norm_rows, rope_cos_sin
 from tinyserve_amd.workloads import fused_case
 
 pytestmark = pytest.mark.gpu
@@ -146,3 +146,32 @@ def test_baseline_config_4(dtype: torch.dtype) -> None:
     assert torch.equal(kc.isnan(), kc_ref.isnan()) and torch.equal(vc.isnan(), vc_ref.isnan())
     assert torch.equal(torch.nan_to_num(kc), torch.nan_to_num(kc_ref))
     assert torch.equal(torch.nan_to_num(vc), torch.nan_to_num(vc_ref))
+
+
+@pytest.mark.parametrize("head_dim", [2, 64, 128, 256])
+@pytest.mark.parametrize("theta", [10_000.0, 1_000_000.0])
+def test_rope_cos_sin_equals_the_reference_tables(head_dim: int, theta: float) -> None:
+    # layers.py:41-65 in float64 on the CPU (the oracle) against the one-launch kernel:
+    # the same float64 angles, cos / sin rounded once to float32. Both libms are within
+    # an ulp of float64, so a table entry may differ only where the float64 result lies
+    # within that of a float32 rounding boundary: at most one float32 ulp, rarely.
+    g = torch.Generator().manual_seed(head_dim)
+    pos = torch.cat([torch.arange(0, 70), torch.randint(0, 40960, (500,), generator=g), torch.tensor([40959])])
+    want_c, want_s = ref.rope_cos_sin(head_dim, theta, pos)
+    got_c, got_s = rope_cos_sin(head_dim, theta, pos.to(DEVICE))
+    for got, want in ((got_c.cpu(), want_c), (got_s.cpu(), want_s)):
+        assert got.shape == want.shape == (pos.numel(), head_dim) and got.dtype == torch.float32
+        assert torch.equal(got[:, : head_dim // 2], got[:, head_dim // 2 :])
+        diff = got != want
+        ulp = torch.finfo(torch.float32).eps * want.abs().clamp_min(2.0**-126)
+        assert bool(((got - want).abs() <= ulp).all())
+        assert int(diff.sum()) <= max(1, want.numel() // 10_000), int(diff.sum())
+
+
+def test_rope_cos_sin_rejects_bad_arguments() -> None:
+    with pytest.raises(ValueError, match="int64"):
+        rope_cos_sin(64, 1e6, torch.arange(4, dtype=torch.int32, device=DEVICE))
+    with pytest.raises(ValueError, match="even"):
+        rope_cos_sin(63, 1e6, torch.arange(4, device=DEVICE))
+    c, s = rope_cos_sin(64, 1e6, torch.empty(0, dtype=torch.int64, device=DEVICE))
+    assert c.shape == s.shape == (0, 64)

@@ -59,6 +59,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          *([_i64] * 11),  # strides
          _f, _i, _i, _vp],
     ),
+    "ts_rope_cos_sin": (_i, [_vp, _i, _i, ctypes.c_double, _vp, _vp, _i64, _vp]),
     "ts_rows_gemm": (_i, [_vp, _i, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _i, _i, _i, _i, _i, _vp]),
     "ts_rows_gemm_plan": (_i, [_i, _i, _i, _i, _c_i32p]),
     "ts_add_rms_norm": (_i, [_vp, _i64, _vp, _i, _vp, _vp, _i64, _vp, _i, _i64, _i, _i, _f, _i, _vp]),

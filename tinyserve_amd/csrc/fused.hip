@@ -306,9 +306,40 @@ static int launch_qk_cache(const QkArgs& a, int D, int cache_dtype, hipStream_t 
   }
 }
 
+// ---------------------------------------------------------------------------------
+// rope_cos_sin: the rotation tables of layers.py:41-65 for T positions, one thread per
+// (position, pair i): inv_freq = theta^(-2i / D) and the angle p * inv_freq in float64,
+// cos / sin in float64 rounded once to float32, written to columns i and i + D/2.
+__global__ __launch_bounds__(256) void rope_cos_sin_kernel(const int64_t* __restrict__ pos, int T, int D,
+                                                           double theta, float* __restrict__ cos_out,
+                                                           float* __restrict__ sin_out, int64_t stride) {
+  const int half = D / 2;
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (u >= static_cast<int64_t>(T) * half) return;
+  const int t = static_cast<int>(u / half), i = static_cast<int>(u % half);
+  const double inv_freq = pow(theta, -static_cast<double>(2 * i) / static_cast<double>(D));
+  const double ang = static_cast<double>(pos[t]) * inv_freq;
+  const float c = static_cast<float>(cos(ang)), sn = static_cast<float>(sin(ang));
+  cos_out[t * stride + i] = c;
+  cos_out[t * stride + i + half] = c;
+  sin_out[t * stride + i] = sn;
+  sin_out[t * stride + i + half] = sn;
+}
+
 }  // namespace ts
 
 using namespace ts;
+
+extern "C" int ts_rope_cos_sin(const int64_t* positions, int T, int D, double theta, float* cos_out,
+                               float* sin_out, int64_t stride, void* stream) {
+  if (T < 0 || D < 2 || D % 2 || stride < D || !(theta > 0.0)) return TS_EINVAL;
+  if (T == 0) return 0;
+  if (!positions || !cos_out || !sin_out) return TS_EINVAL;
+  const int64_t n = static_cast<int64_t>(T) * (D / 2);
+  hipLaunchKernelGGL(rope_cos_sin_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), positions, T, D, theta, cos_out, sin_out, stride);
+  return launch_status();
+}
 
 extern "C" int ts_rms_norm_rows(const void* x, const void* w, void* out, int T, int N,
                                 int64_t x_stride, int64_t o_stride, float eps, int dtype,

@@ -119,11 +119,9 @@ class KVPool:
 
 def rope_tables(head_dim: int, theta: float, positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """``[T, D]`` float32 cos / sin on the positions' device, angles in float64 (the
-    reference's ``rope_cos_sin``, layers.py:41-65; positions reach 40960)."""
-    inv_freq = theta ** (-torch.arange(0, head_dim, 2, dtype=torch.float64, device=positions.device) / head_dim)
-    ang = positions.to(torch.float64)[:, None] * inv_freq[None, :]
-    ang = torch.cat([ang, ang], dim=-1)
-    return ang.cos().float(), ang.sin().float()
+    reference's ``rope_cos_sin``, layers.py:41-65; positions reach 40960): one launch of
+    ``hip_fused.rope_cos_sin``."""
+    return hip_fused.rope_cos_sin(head_dim, theta, positions.to(torch.int64))
 
 
 class DecodeStep:

@@ -1,7 +1,8 @@
 """Fused per-layer kernels around attention on MI355X: ``rms_norm_rows`` and
 ``qk_norm_rope_store`` of the reference's ``tinyserve.triton_fused``
 (src/tinyserve/triton_fused.py:116-177), same arguments, results and errors, launching
-``csrc/fused.hip``.
+``csrc/fused.hip``; and ``rope_cos_sin``, the reference's per-step RoPE tables
+(layers.py:41-65) as one launch.
 
 ``rms_norm_rows``: one wave64 per row, the row held in registers as 16-byte vectors,
 one HBM read and one write per element.
@@ -108,3 +109,21 @@ def qk_norm_rope_store(
             float(eps), _lib.dtype_code(q), _lib.dtype_code(k_cache), _lib.stream_of(dev),
         )  # fmt: skip
     return out
+
+
+def rope_cos_sin(head_dim: int, theta: float, positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``layers.rope_cos_sin`` in one launch: ``(cos, sin)``, each ``[T, head_dim]``
+    float32, ``cat([angles, angles], -1)`` with angles in float64."""
+    if positions.dim() != 1 or positions.dtype != torch.int64:
+        raise ValueError(f"positions must be a [T] int64 tensor, got {positions.dtype} {tuple(positions.shape)}")
+    if head_dim < 2 or head_dim % 2:
+        raise ValueError(f"head_dim must be even, got {head_dim}")
+    t = positions.shape[0]
+    cos = torch.empty(t, head_dim, dtype=torch.float32, device=positions.device)
+    sin = torch.empty_like(cos)
+    if t:
+        dev = _lib.require_device(positions)
+        pos = positions.contiguous()
+        _lib.call("ts_rope_cos_sin", pos.data_ptr(), t, head_dim, float(theta),
+                  cos.data_ptr(), sin.data_ptr(), cos.stride(0), _lib.stream_of(dev))  # fmt: skip
+    return cos, sin
