@@ -229,6 +229,16 @@ def cpu_baselines_other_configs(budget_s: float = 8.0) -> dict:
     return res
 
 
+def check(got: torch.Tensor, want: torch.Tensor, bound: float, what: str) -> float:
+    """Max-abs difference of two results of one workload by two paths (outside any
+    timed region); a difference above ``bound`` stops the benchmark: a number for a
+    wrong result is no number."""
+    diff = float((got.float() - want.float()).abs().max())
+    if not diff <= bound:
+        raise SystemExit(f"bench check failed: {what}: max-abs {diff:.3g} > {bound}")
+    return round(diff, 6)
+
+
 def kernel_name(plan: dict, dtype: str = "f16") -> str:
     """The decode kernel instantiation the library dispatches for ``plan``."""
     budget = {"heavy": "heavy", "light": "light", "light_stream": "light-stream"}[plan["budget"]]
@@ -270,7 +280,9 @@ def extra_measurements() -> dict:
     # (each sequence split over the waves of a workgroup, merged in LDS).
     c = decode_bench_case(32, 256, pool_blocks=4096, device=dev, seed=1)
     nb = decode_bytes(32, 256)["step"]
+    outs = {}
     for key, splits in (("decode_b32_ctx256_s4", 4), ("decode_b32_ctx256_policy", None)):
+        outs[key] = launch_paged_decode_split(*c.args(), c.scale, BS, num_splits=splits).clone()
         def call() -> None:
             launch_paged_decode_split(*c.args(), c.scale, BS, num_splits=splits)
 
@@ -281,14 +293,19 @@ def extra_measurements() -> dict:
                     "launches": "split kernel + combine" if splits else "one launch",
                     "kernel": kernel_name(plan), "grid": plan["grid"],
                     "waves_per_group": plan["waves_per_group"]}  # fmt: skip
+    res["decode_b32_ctx256_policy"]["max_abs_vs_s4"] = check(
+        outs["decode_b32_ctx256_policy"], outs["decode_b32_ctx256_s4"], 4e-3, "config 2: policy vs 4 splits")
     # The reference's own published decode shapes (fp16, one layer, Qwen3 heads; its T4
     # timings in BASELINE.md): B=32 x 1024, B=32 x 160, B=64 x 1024, the policy's launch.
     for b, ctx in ((32, 1024), (32, 160), (64, 1024)):
         cr = decode_bench_case(b, ctx, device=dev, seed=2)
         ms_r = graph_ms(lambda: launch_paged_decode_split(*cr.args(), cr.scale, BS))
         nb_r = decode_bytes(b, ctx)["step"]
+        got = launch_paged_decode_split(*cr.args(), cr.scale, BS).clone()
+        s4 = launch_paged_decode_split(*cr.args(), cr.scale, BS, num_splits=4)
         res[f"decode_b{b}_ctx{ctx}"] = {"us": round(ms_r * 1e3, 2), "GB/s": round(nb_r / ms_r / 1e6, 1),
-                                        "timing": "graph replay"}  # fmt: skip
+                                        "timing": "graph replay",
+                                        "max_abs_vs_s4": check(got, s4, 4e-3, f"decode {b} x {ctx}")}  # fmt: skip
     # Config 3: varlen prefill, 32 prompts L ~ U[16, 2048], fp16 and bf16.
     lens = prefill_lengths(32, seed=0)
     flops = sum(4 * HQ * D * n * (n + 1) // 2 for n in lens)
@@ -304,24 +321,29 @@ def extra_measurements() -> dict:
         if dt == torch.float16:  # the reference's batched SDPA path on the same input
             ref_out = torch.empty_like(p.q)
             ms_ref = loop_ms(lambda: batched_sdpa_prefill(p, ref_out), 5, 1)
-            diff = (ref_out.float() - out.float()).abs().max()  # `out` holds the HIP result
             res["prefill_varlen32_reference_batched_sdpa_fp32"] = {
                 "ms": round(ms_ref, 3), "TFLOP/s": round(flops / ms_ref / 1e9, 1),
                 "hip_kernel_speedup": round(ms_ref / ms, 1),
-                "max_abs_diff_vs_hip": float(diff)}  # fmt: skip
+                "max_abs_diff_vs_hip": check(out, ref_out, 4e-3, "config 3 vs batched SDPA")}  # fmt: skip
     # 2048-token prompts: a batch of 4 (fills the chip) and one alone (the critical path).
     four = prefill_case([(0, 2048)] * 4, HQ, HKV, D, BS, torch.float16, sentinel=False, device=dev)
     out4 = torch.empty_like(four.q)
     ms = loop_ms(lambda: paged_prefill_attention(*four.args(), out=out4), 20, 3)
     f4 = 4 * 4 * HQ * D * 2048 * 2049 // 2
     res["prefill_4x2048_float16"] = {"ms": round(ms, 4), "TFLOP/s": round(f4 / ms / 1e9, 1),
-                                     "mfma_frac": round(f4 / ms / 1e9 / FP16_PEAK_TFLOPS, 4)}
+                                     "mfma_frac": round(f4 / ms / 1e9 / FP16_PEAK_TFLOPS, 4),
+                                     "max_abs_vs_batched_sdpa": check(
+                                         out4, batched_sdpa_prefill(four, torch.empty_like(four.q)), 4e-3,
+                                         "prefill 4 x 2048")}  # fmt: skip
     one = prefill_case([(0, 2048)], HQ, HKV, D, BS, torch.float16, sentinel=False, device=dev)
     out = torch.empty_like(one.q)
     ms = loop_ms(lambda: paged_prefill_attention(*one.args(), out=out), 20, 3)
     f1 = 4 * HQ * D * 2048 * 2049 // 2
     res["prefill_single2048_float16"] = {"ms": round(ms, 4), "TFLOP/s": round(f1 / ms / 1e9, 1),
-                                         "mfma_frac": round(f1 / ms / 1e9 / FP16_PEAK_TFLOPS, 4)}
+                                         "mfma_frac": round(f1 / ms / 1e9 / FP16_PEAK_TFLOPS, 4),
+                                         "max_abs_vs_batched_sdpa": check(
+                                             out, batched_sdpa_prefill(one, torch.empty_like(one.q)), 4e-3,
+                                             "prefill 1 x 2048")}  # fmt: skip
     # Config 4: fused RMSNorm + q/k norm + RoPE + KV write, T=4096.
     f = fused_case(device=dev, sentinel=False)
     def rms() -> None:
@@ -334,7 +356,11 @@ def extra_measurements() -> dict:
     ms_r, ms_q = graph_ms(rms), graph_ms(qk)
     t = 4096
     b_r, b_q = t * 1024 * 2 * 2, t * 16904
+    # layers.py:34-38 restated with torch ops on the GPU (normalise in fp32, round, times w).
+    xf = f.x.float()
+    want_rms = (xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + f.eps)).to(f.x.dtype) * f.norm_w
     res["fused_t4096"] = {
+        "rms_max_abs_vs_torch": check(rms_norm_rows(f.x, f.norm_w, f.eps), want_rms, 2e-2, "rms_norm_rows"),
         "rms_norm_rows_us": round(ms_r * 1e3, 2), "rms_GB/s": round(b_r / ms_r / 1e6, 1),
         "qk_norm_rope_store_us": round(ms_q * 1e3, 2), "qk_GB/s": round(b_q / ms_q / 1e6, 1),
         "bytes": b_r + b_q, "timing": "graph replay of 20 launches",
@@ -379,12 +405,16 @@ def decode_step_28l(batch: int = 64, steps: int = 20, seed: int = 5, ctx: tuple[
     kv_bytes = sum(lens) * shape.num_layers * 2 * shape.kv_size * 2
     res: dict = {"batch": batch, "ctx_mean": round(sum(lens) / batch, 1), "kv_read_GB": round(kv_bytes / 1e9, 2),
                  "table_width": inp.block_tables.shape[1]}  # fmt: skip
+    # Each replay writes the same new tokens' k/v to the same slots, so every replay and
+    # every variant sees the same cache: their logits can be compared directly.
+    logits = {}
     for splits, projections in variants:
         step = DecodeStep(shape, w, pool, splits, projections)
         full = DecodeGraph(step.forward, inp)
         attn = DecodeGraph(step.attention_only, inp)
         ms_step = loop_ms(full.replay, steps, 3)
         ms_attn = loop_ms(attn.replay, steps, 3)
+        logits[(splits, projections)] = full.replay().clone()
         used = splits or num_splits_for(batch, shape.num_kv_heads, inp.block_tables.shape[1])
         plan = decode_plan(batch, HQ, HKV, D, BS, inp.block_tables.shape[1], 1 if splits is None and used <= 4 else used)
         key = f"splits_{used}" + ("" if projections == "rows" else f"_{projections}_projections")
@@ -393,6 +423,12 @@ def decode_step_28l(batch: int = 64, steps: int = 20, seed: int = 5, ctx: tuple[
                                  "attention_GB/s": round(kv_bytes / ms_attn / 1e6, 1),
                                  "kernel": kernel_name(plan), "projections": projections}  # fmt: skip
         del full, attn
+    base = logits[variants[0]]
+    for key, out in list(logits.items())[1:]:
+        # fp16 steps by other split counts / projection kernels: ~1e-2 of drift over 28
+        # layers (the tests bound each against the fp32 composition at 0.05).
+        res[f"logits_max_abs_{key[0] or 'policy'}_{key[1]}_vs_{variants[0][0] or 'policy'}_{variants[0][1]}"] = check(
+            out, base, 0.1, f"decode step {key} vs {variants[0]}")  # fmt: skip
     return res
 
 
