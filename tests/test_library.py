@@ -70,6 +70,41 @@ def test_c_abi_rejects_bad_sizes_before_any_launch(lib: ctypes.CDLL) -> None:
     # empty batches launch nothing and succeed
     assert lib.ts_decode_split(*([null] * 9), 0, 4, 2, 32, 16, *strides, 0, 1, 0, 1.0, 0, null) == 0
     assert lib.ts_rms_norm_rows(null, null, null, 0, 16, 16, 16, 1e-6, 1, null) == 0
+    # RoPE tables: odd head dim, a row stride shorter than the head dim, a theta of 0
+    assert lib.ts_rope_cos_sin(null, 4, 63, 1e6, null, null, 64, null) == -1
+    assert lib.ts_rope_cos_sin(null, 4, 64, 1e6, null, null, 32, null) == -1
+    assert lib.ts_rope_cos_sin(null, 4, 64, 0.0, null, null, 64, null) == -1
+    assert lib.ts_rope_cos_sin(null, 0, 64, 1e6, null, null, 64, null) == 0
+    # The decode step's projections: missing operands, an unknown epilogue, strides
+    # shorter than a row, a tiled x whose width is not a multiple of 32.
+    p = ctypes.c_void_p(16)  # a non-null stand-in; never dereferenced on these paths
+    assert lib.ts_rows_gemm(null, 0, 64, p, 64, p, 64, null, 0, 4, 64, 64, 0, 1, null) == -1
+    assert lib.ts_rows_gemm(p, 0, 64, p, 64, p, 64, null, 0, 4, 64, 64, 3, 1, null) == -1
+    assert lib.ts_rows_gemm(p, 0, 32, p, 64, p, 64, null, 0, 4, 64, 64, 0, 1, null) == -1
+    assert lib.ts_rows_gemm(p, 1, 0, p, 48, p, 64, null, 0, 4, 64, 48, 0, 1, null) == -1
+    assert lib.ts_rows_gemm(p, 0, 64, p, 64, p, 64, null, 0, 0, 64, 64, 0, 1, null) == 0  # no rows
+    # fp32 has no MFMA projection kernel
+    assert lib.ts_rows_gemm(p, 0, 64, p, 64, p, 64, null, 0, 4, 64, 64, 0, 0, null) == -2
+    assert lib.ts_add_rms_norm(p, 64, null, 2, p, p, 64, p, 0, 64, 4, 64, 1e-6, 1, null) == -1  # ks, no partials
+    assert lib.ts_add_rms_norm(p, 32, null, 0, p, p, 64, p, 0, 64, 4, 64, 1e-6, 1, null) == -1  # short stride
+    assert lib.ts_add_rms_norm(p, 64, null, 0, p, p, 64, p, 0, 64, 0, 64, 1e-6, 1, null) == 0  # no rows
+    out = (ctypes.c_int * 5)()
+    assert lib.ts_rows_gemm_plan(64, 4096, 48, 0, out) == -2  # K not a multiple of 32
+    assert lib.ts_rows_gemm_plan(64, 4096, 1024, 7, out) == -1
+
+
+def test_projection_launch_plans(lib: ctypes.CDLL) -> None:
+    # The projection kernels' launch shapes at Qwen3-0.6B's sizes (64 rows): sizes only.
+    out = (ctypes.c_int * 5)()
+    for (n, k, epi), want in {
+        (4096, 1024, 0): (8, 1, 4, 1, 1),   # qkv: one K slice, 256 workgroups
+        (1024, 2048, 1): (4, 2, 2, 8, 1),   # o_proj: 8 K slices
+        (3072, 1024, 2): (8, 2, 4, 1, 1),   # gate_up + SiLU
+        (1024, 3072, 1): (8, 2, 2, 6, 1),   # down_proj: 6 K slices
+        (64, 96, 2): (1, 2, 1, 1, 3),        # small: one wave, three 32-column chunks
+    }.items():
+        assert lib.ts_rows_gemm_plan(64, n, k, epi, out) == 0
+        assert tuple(out) == want, (n, k, epi, tuple(out))
 
 
 def test_decode_launch_plans(lib: ctypes.CDLL) -> None:
