@@ -168,3 +168,18 @@ def test_arguments_are_checked() -> None:
         add_rms_norm(x, None, w[0].float(), EPS)
     with pytest.raises(ValueError, match="KS"):
         add_rms_norm(x, torch.zeros(2, 4, 32, device=DEVICE), w[0], EPS)
+    # Caller-provided outputs must be exactly what the kernel writes.
+    with pytest.raises(ValueError, match="out must be"):
+        rows_linear(x, w, out=torch.empty(4, 32, dtype=torch.float16, device=DEVICE))
+    with pytest.raises(ValueError, match="out must be"):
+        rows_linear(x, w, out=torch.empty(4, 64, dtype=torch.float32, device=DEVICE))
+    with pytest.raises(ValueError, match="partial"):
+        rows_linear_partials(x, w, torch.empty(4 * 64 * 16, dtype=torch.float16, device=DEVICE))
+    with pytest.raises(ValueError, match="Tiled"):
+        rows_silu_gate_up(x, w, out=torch.empty(4, 32, dtype=torch.float16, device=DEVICE))
+    with pytest.raises(ValueError, match="operand-tiled"):
+        rows_silu_gate_up(x, w, out=Tiled.empty(4, 64, torch.float16, torch.device(DEVICE)))
+    with pytest.raises(ValueError, match="h must be"):
+        add_rms_norm(x, None, w[0], EPS, tiled=True, h=torch.empty_like(x))
+    with pytest.raises(ValueError, match="h must be"):
+        add_rms_norm(x, None, w[0], EPS, tiled=True, h=Tiled.empty(8, 64, torch.float16, torch.device(DEVICE)))

@@ -94,10 +94,30 @@ def supported(dtype: torch.dtype) -> bool:
 def _x_args(x: torch.Tensor | Tiled) -> tuple[int, int, int, int, int]:
     """(pointer, tiled, row stride, rows, cols) of a projection's input."""
     if isinstance(x, Tiled):
+        if x.cols % 32 or x.buf.numel() < padded_rows(x.rows) * x.cols or not x.buf.is_contiguous():
+            raise ValueError(f"x: an operand-tiled [{x.rows}, {x.cols}] needs a contiguous buffer of "
+                             f"{padded_rows(x.rows) * x.cols} elements and a multiple of 32 columns")  # fmt: skip
         return x.buf.data_ptr(), 1, 0, x.rows, x.cols
     if x.dim() != 2 or x.stride(1) != 1:
         raise ValueError("x must be [M, K] with unit column stride")
     return x.data_ptr(), 0, x.stride(0), x.shape[0], x.shape[1]
+
+
+def _check_out(t: torch.Tensor | Tiled, rows: int, cols: int, dtype: torch.dtype, dev: int, what: str) -> None:
+    """A caller-provided output must be exactly what the kernel writes: the kernels see
+    raw pointers and would write past a smaller buffer."""
+    if isinstance(t, Tiled):
+        if (t.rows, t.cols) != (rows, cols) or t.buf.numel() < padded_rows(rows) * cols:
+            raise ValueError(f"{what} must be an operand-tiled [{rows}, {cols}], got [{t.rows}, {t.cols}]")
+        if not t.buf.is_contiguous():
+            raise ValueError(f"{what}'s buffer must be contiguous")
+        t = t.buf
+    elif tuple(t.shape) != (rows, cols) or t.stride(1) != 1:
+        raise ValueError(f"{what} must be [{rows}, {cols}] with unit column stride, got {tuple(t.shape)}")
+    if t.dtype != dtype:
+        raise ValueError(f"{what} must be {dtype}, got {t.dtype}")
+    if _lib.require_device(t) != dev:
+        raise ValueError(f"{what} is on another device")
 
 
 def _check(x: torch.Tensor | Tiled, w: torch.Tensor) -> int:
@@ -118,6 +138,7 @@ def rows_linear(x: torch.Tensor | Tiled, w: torch.Tensor, out: torch.Tensor | No
         raise ValueError(f"x has {k} columns but w is {tuple(w.shape)}")
     if out is None:
         out = torch.empty(m, n, dtype=w.dtype, device=w.device)
+    _check_out(out, m, n, w.dtype, dev, "out")
     _lib.call("ts_rows_gemm", xp, xt, xs, w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0), None, 0,
               m, n, k, ROWS_STORE, _lib.dtype_code(w), _lib.stream_of(dev))  # fmt: skip
     return out
@@ -136,11 +157,14 @@ def rows_linear_partials(x: torch.Tensor | Tiled, w: torch.Tensor,
     if plan is None:
         raise ValueError(f"no projection shape for M={m}, N={n}, K={k}")
     ks = plan["k_splits"]
+    if partial is not None and (partial.dtype != torch.float32 or not partial.is_contiguous()
+                                or _lib.require_device(partial) != dev):  # fmt: skip
+        raise ValueError("partial must be a contiguous float32 buffer on x's device")
     if partial is None or partial.numel() < ks * m * n:
         partial = torch.empty(ks * m * n, dtype=torch.float32, device=w.device)
     _lib.call("ts_rows_gemm", xp, xt, xs, w.data_ptr(), w.stride(0), None, 0, partial.data_ptr(),
               partial.numel(), m, n, k, ROWS_PARTIAL, _lib.dtype_code(w), _lib.stream_of(dev))  # fmt: skip
-    return partial[: ks * m * n].view(ks, m, n), ks
+    return partial.view(-1)[: ks * m * n].view(ks, m, n), ks
 
 
 def rows_silu_gate_up(x: torch.Tensor | Tiled, w_gate_up: torch.Tensor, out: Tiled | None = None) -> Tiled:
@@ -153,6 +177,9 @@ def rows_silu_gate_up(x: torch.Tensor | Tiled, w_gate_up: torch.Tensor, out: Til
     n = w_gate_up.shape[0] // 2
     if out is None:
         out = Tiled.empty(m, n, w_gate_up.dtype, w_gate_up.device)
+    if not isinstance(out, Tiled):
+        raise ValueError("out must be a Tiled (the SiLU epilogue writes the operand-tiled layout)")
+    _check_out(out, m, n, w_gate_up.dtype, dev, "out")
     _lib.call("ts_rows_gemm", xp, xt, xs, w_gate_up.data_ptr(), w_gate_up.stride(0), out.buf.data_ptr(), 0,
               None, 0, m, n, k, ROWS_SILU, _lib.dtype_code(w_gate_up), _lib.stream_of(dev))  # fmt: skip
     return out
@@ -177,6 +204,9 @@ def add_rms_norm(x: torch.Tensor, partial: torch.Tensor | None, weight: torch.Te
     dev = _lib.require_device(x, weight, *(() if partial is None else (partial,)))
     if h is None:
         h = Tiled.empty(m, n, x.dtype, x.device) if tiled else torch.empty_like(x)
+    if isinstance(h, Tiled) != tiled:
+        raise ValueError(f"h must be {'a Tiled' if tiled else 'a row-major tensor'} (tiled={tiled})")
+    _check_out(h, m, n, x.dtype, dev, "h")
     hp = h.buf.data_ptr() if isinstance(h, Tiled) else h.data_ptr()
     hs = 0 if isinstance(h, Tiled) else h.stride(0)
     _lib.call("ts_add_rms_norm", x.data_ptr(), x.stride(0), None if partial is None else partial.data_ptr(), ks,
