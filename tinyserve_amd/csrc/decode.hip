@@ -554,9 +554,45 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ m
                                                      int Hq, int D, int64_t o_sb, int64_t o_sh,
                                                      int splits) {
   constexpr int kU = 8;  // splits whose loads are in flight together
+  constexpr int kFew = 16;  // up to this many splits: every load issued at once
   const int lane = threadIdx.x;
   const int b = blockIdx.x, h = blockIdx.y;
   const int64_t base = (static_cast<int64_t>(b) * Hq + h) * splits;
+  if (splits <= kFew) {
+    // One round trip: the maxima, denominators and every partial sum are loaded before
+    // any is used; then the same operations, in the same order, as the general path.
+    const bool mine = lane < splits;
+    const float mv = mine ? m[base + lane] : -INFINITY;
+    const float lv = mine ? l[base + lane] : 0.f;
+    float x[kFew][ED];
+#pragma unroll
+    for (int u = 0; u < kFew; ++u)
+#pragma unroll
+      for (int e = 0; e < ED; ++e) {
+        const int d = lane + kWave * e;
+        x[u][e] = u < splits && d < D ? acc[(base + u) * D + d] : 0.f;
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    const float mmax = wave_max(mv);
+    const float wgt = mine ? fast_exp2(mv - mmax) : 0.f;
+    const float den = group_sum<kWave>(mine ? fmaf(wgt, lv, 0.f) : 0.f);
+    float num[ED];
+#pragma unroll
+    for (int e = 0; e < ED; ++e) num[e] = 0.f;
+#pragma unroll
+    for (int u = 0; u < kFew; ++u) {
+      const float w = __shfl(wgt, u);  // 0 past the last split
+#pragma unroll
+      for (int e = 0; e < ED; ++e) num[e] = fmaf(w, x[u][e], num[e]);
+    }
+    T* op = out + b * o_sb + h * o_sh;
+#pragma unroll
+    for (int e = 0; e < ED; ++e) {
+      const int d = lane + kWave * e;
+      if (d < D) op[d] = from_f32<T>(num[e] / den);
+    }
+    return;
+  }
   float mmax = -INFINITY;
   for (int s0 = 0; s0 < splits; s0 += kWave)
     if (s0 + lane < splits) mmax = fmaxf(mmax, m[base + s0 + lane]);
