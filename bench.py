@@ -458,7 +458,8 @@ def main() -> None:
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--profile", choices=["prefill_varlen32", "fused_t4096", "decode_b32_ctx256"], default=None,
+    ap.add_argument("--profile", choices=["prefill_varlen32", "fused_t4096", "decode_b32_ctx256",
+                                          "step_projections"], default=None,
                     help="only launch one workload 3 times (for a profiler) and print what ran")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run 3 plain device copies of this many MiB (a known-size kernel "
@@ -490,6 +491,10 @@ def main() -> None:
                 launch_paged_decode_split(*c.args(), c.scale, BS, num_splits=splits)
         torch.cuda.synchronize()
         print(json.dumps({"profile": args.profile, "launches": "20 x (split kernel + combine), then 20 x one launch",
+                          **calibration_copies(args.copy_mb)}), flush=True)  # fmt: skip
+        return
+    if args.profile == "step_projections":  # config 5's four projections of a layer, W cold
+        print(json.dumps({"profile": args.profile, **step_projections_for_profile(),
                           **calibration_copies(args.copy_mb)}), flush=True)  # fmt: skip
         return
     if args.profile == "fused_t4096":  # config 4's two fused kernels, eager, nothing else
@@ -552,6 +557,36 @@ def main() -> None:
         line["extra"] = extra_measurements()
     line.update(calibration_copies(args.copy_mb))
     print(json.dumps(line), flush=True)
+
+
+def step_projections_for_profile(rows: int = 64, dispatches: int = 24) -> dict:
+    """The config-5 layer's four projections on the row-batch kernels (qkv, o_proj with
+    8 K slices, gate_up + SiLU, down_proj with 6), fp16, 64 rows, each launched
+    ``dispatches`` times over as many weight copies, more than the 256 MiB last-level
+    cache holds between two uses of one copy, so W comes from HBM as in the step."""
+    from tinyserve_amd import hip_rows as R
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    out: dict = {}
+    for name, (n, k) in {"qkv": (4096, 1024), "o_proj": (1024, 2048), "gate_up": (6144, 1024),
+                         "down_proj": (1024, 3072)}.items():  # fmt: skip
+        ws = [torch.randn(n, k, generator=g, device=dev).half() for _ in range(max(dispatches, (320 << 20) // (n * k * 2)))]
+        x = torch.randn(rows, k, generator=g, device=dev).half()
+        xt = R.Tiled.from_dense(x)
+        for w in ws[:dispatches]:
+            if name == "qkv":
+                R.rows_linear(xt, w)
+            elif name == "o_proj":
+                R.rows_linear_partials(x, w)
+            elif name == "gate_up":
+                R.rows_silu_gate_up(xt, w)
+            else:
+                R.rows_linear_partials(xt, w)
+        torch.cuda.synchronize()
+        out[name] = {"W_bytes": n * k * 2, "dispatches": dispatches, "copies": len(ws)}
+        del ws
+    return out
 
 
 def calibration_copies(mb: int) -> dict:
