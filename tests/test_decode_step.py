@@ -28,6 +28,9 @@ DEVICE = "cuda"
 # 0.019 at 16 splits and 0.021 with the policy, logits up to 3.2 in magnitude); the bound
 # leaves 2.5x that.
 LOGITS_ATOL = 0.05
+# The 2-layer tiny model's 16-bit logits against the fp32 composition: measured 0.0010-0.0012
+# (fp16) and 0.0077-0.0080 (bf16) on both projection paths; the bounds leave ~4x that.
+TINY_LOGITS_ATOL = {torch.float16: 5e-3, torch.bfloat16: 3e-2}
 TINY = ModelShape(hidden=256, num_heads=4, num_kv_heads=2, head_dim=64, intermediate=512, vocab=1000,
                   num_layers=2)  # fmt: skip
 
@@ -176,6 +179,28 @@ def test_mixed_step_matches_the_reference_step(cached: list[int], new: list[int]
     torch.testing.assert_close(pool.v.cpu()[:, slots], vr[:, slots], atol=1e-5, rtol=1e-5)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_mixed_step_row_projections_match_the_reference_step(dtype: torch.dtype) -> None:
+    # forward_batch (prefill and decode sequences in one step) in 16-bit types: the
+    # row-batch projection kernels (up to 256 rows) and library GEMMs, each against the
+    # oracle-composed fp32 step.
+    cached, new = [5, 0, 9, 2, 0], [3, 7, 1, 1, 40]
+    outs = {}
+    for projections in ("rows", "library"):
+        w, pool, tabs, _ = setup([c + n for c, n in zip(cached, new)], len(cached), dtype, seed=17)
+        g = torch.Generator(device="cpu").manual_seed(19)
+        items = [(torch.randint(0, TINY.vocab, (n,), generator=g).tolist(), t) for n, t in zip(new, tabs)]
+        batch = build_batch(items, DEVICE)
+        kr, vr = pool.k.float().cpu(), pool.v.float().cpu()
+        want = reference_step(TINY, w, kr, vr, batch, pool.block_size)[batch.last_rows.cpu()]
+        step = DecodeStep(TINY, w, pool, None, projections)
+        outs[projections] = step.forward_batch(batch).cpu()
+        err = (outs[projections] - want).abs().max().item()
+        print(f"[mixed {dtype}] {projections}: logits max-abs {err:.3g} vs fp32")
+        torch.testing.assert_close(outs[projections], want, atol=TINY_LOGITS_ATOL[dtype], rtol=0)
+    torch.testing.assert_close(outs["rows"], outs["library"], atol=TINY_LOGITS_ATOL[dtype], rtol=0)
+
+
 def test_mixed_step_equals_each_sequence_alone() -> None:
     # test_batched_forward.py: a sequence's logits do not depend on what else is batched.
     cached, new = [4, 0, 11, 7], [1, 9, 1, 5]
@@ -301,12 +326,12 @@ def test_row_projections_match_the_reference_step(dtype: torch.dtype, rows: int)
         outs[projections] = step.forward(inp)[: len(lens)].cpu()
         err = (outs[projections] - want).abs().max().item()
         print(f"[tiny {dtype}] {projections}: logits max-abs {err:.3g} vs fp32")
-        torch.testing.assert_close(outs[projections], want, atol=0.05 if dtype == torch.float16 else 0.2, rtol=0)
+        torch.testing.assert_close(outs[projections], want, atol=TINY_LOGITS_ATOL[dtype], rtol=0)
         # The new tokens' k/v went to the cache (the v copy through the fused kernel).
         real = inp.slots.cpu()[: len(lens)]
         torch.testing.assert_close(pool.v.float().cpu()[:, real], vr[:, real],
                                    atol=2e-3 if dtype == torch.float16 else 2e-2, rtol=2e-2)  # fmt: skip
-    torch.testing.assert_close(outs["rows"], outs["library"], atol=0.05 if dtype == torch.float16 else 0.2, rtol=0)
+    torch.testing.assert_close(outs["rows"], outs["library"], atol=TINY_LOGITS_ATOL[dtype], rtol=0)
 
 
 def test_projection_choice() -> None:
