@@ -332,13 +332,15 @@ static int dispatch_rows(const RowsArgs& a, const RowsPlan& p, bool xt, hipStrea
 // ---- add_rms_norm -----------------------------------------------------------------------
 // One wave per row; lane l holds 8-element chunks l, l + 64, ... (CPL of them).
 template <typename T, int CPL>
-__global__ __launch_bounds__(256) void add_rms_norm_kernel(const T* __restrict__ x, const float* __restrict__ part,
+__global__ __launch_bounds__(64) void add_rms_norm_kernel(const T* __restrict__ x, const float* __restrict__ part,
                                                            int ks, const T* __restrict__ w, T* xo,
                                                            T* __restrict__ h, bool h_tiled, int M, int rows,
                                                            int N, int64_t xs, int64_t xos, int64_t hs,
                                                            float eps) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int row = blockIdx.x * 4 + static_cast<int>(threadIdx.x >> 6);
+  // One wave per workgroup: a decode step's few rows land on as many CUs, each pulling
+  // only its row's partials through its own L1.
+  const int row = blockIdx.x;
   if (row >= rows) return;
   if (row >= M) {
     // Padding rows of an operand-tiled output (read whole by the projection): zeros.
@@ -436,7 +438,7 @@ static int launch_add_rms(const void* x, int64_t xs, const float* part, int ks, 
                           hipStream_t st) {
   const int cpl = (N + kWave * 8 - 1) / (kWave * 8);
   const int rows = h_tiled ? (M + kRowBlock - 1) / kRowBlock * kRowBlock : M;
-  const dim3 grid((rows + 3) / 4), block(256);
+  const dim3 grid(rows), block(kWave);
   const T* xp = static_cast<const T*>(x);
   const T* wp = static_cast<const T*>(w);
   T* xop = static_cast<T*>(xo);
