@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const T* __restrict_
                                                             float eps) {
   constexpr int VEC = ALIGNED ? 16 / static_cast<int>(sizeof(T)) : 1;
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= rows) return;
   const T* xr = x + row * xs;
   // The row and the weight are loaded together: the weight's round trip then overlaps
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void rms_norm_rows_long_kernel(const T* __rest
                                                                  int N, int64_t xs, int64_t os,
                                                                  float eps) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= rows) return;
   const T* xr = x + row * xs;
   float ss = 0.f;
@@ -125,7 +125,10 @@ static int launch_rms(const void* x, const void* w, void* out, int rows, int N, 
   const T* xp = static_cast<const T*>(x);
   const T* wp = static_cast<const T*>(w);
   T* op = static_cast<T*>(out);
-  dim3 grid((rows + 3) / 4), block(256);
+  // Fewer rows than four per CU (a decode step's batch): one wave per workgroup, so the
+  // rows spread over as many CUs; otherwise four waves (rows) per workgroup.
+  const int wpb = rows < 4 * compute_units() ? 1 : 4;
+  dim3 grid((rows + wpb - 1) / wpb), block(64 * wpb);
   const int per_chunk = 64 * (aligned ? VEC : 1);
   const int cpl = (N + per_chunk - 1) / per_chunk;
 #define TS_RMS(C, A) \
