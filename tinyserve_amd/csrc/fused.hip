@@ -278,7 +278,9 @@ static int launch_qk_d(const QkArgs& a, hipStream_t st) {
   const uintptr_t pc = reinterpret_cast<uintptr_t>(a.kc) | reinterpret_cast<uintptr_t>(a.vc);
   aligned &= pt % (W * sizeof(T)) == 0 && pc % (W * sizeof(TC)) == 0;
   const int64_t threads = static_cast<int64_t>(a.T) * (a.Hq + 2 * a.Hkv) * LPH;
-  dim3 grid(static_cast<unsigned>((threads + 255) / 256)), block(256);
+  // Few tokens (a decode step): one-wave workgroups, spread over more CUs.
+  const int bt = threads < 256 * static_cast<int64_t>(compute_units()) ? 64 : 256;
+  dim3 grid(static_cast<unsigned>((threads + bt - 1) / bt)), block(bt);
   if (aligned)
     hipLaunchKernelGGL((qk_norm_rope_store_kernel<T, TC, D, true>), grid, block, 0, st, a);
   else
