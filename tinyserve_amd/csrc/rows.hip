@@ -251,10 +251,10 @@ struct RowsPlan {
 // Candidate (KP, NTW, STEPS) per epilogue, in order of preference; KS then follows from
 // K. Measured on MI355X at Qwen3-0.6B shapes with 64 rows and W read cold from HBM
 // (fp16, graph replay, us per launch; the library GEMM in brackets):
-//   qkv     N 4096, K 1024, kStore, x tiled:         8 waves x 1 tile x 4 steps, KS 1: 5.5 (11.4)
-//   o_proj  N 1024, K 2048, kPartial, x row-major:   4 waves x 2 tiles x 2 steps, KS 8: 4.6 (10.6)
-//   gate_up N 2 x 3072, K 1024, SiLU, x tiled:       8 waves x 2 tiles x 4 steps, KS 1: 6.7 (11.9)
-//   down    N 1024, K 3072, kPartial, x tiled:       8 waves x 2 tiles x 2 steps, KS 6: 4.8 (9.3)
+//   qkv     N 4096, K 1024, kStore, x tiled:         8 waves x 1 tile x 4 steps, KS 1: 5.7 (11.5)
+//   o_proj  N 1024, K 2048, kPartial, x row-major:   4 waves x 2 tiles x 2 steps, KS 8: 4.7 (10.6)
+//   gate_up N 2 x 3072, K 1024, SiLU, x tiled:       8 waves x 2 tiles x 4 steps, KS 1: 7.6 (11.7)
+//   down    N 1024, K 3072, kPartial, x tiled:       8 waves x 2 tiles x 2 steps, KS 6: 5.1 (9.3)
 // Across these, ~256 workgroups (one per CU) with each wave's loads in one round trip
 // was the best shape; fewer, larger workgroups or more K splits were slower.
 constexpr int kMaxSplits = 16;
