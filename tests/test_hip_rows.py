@@ -183,3 +183,31 @@ def test_arguments_are_checked() -> None:
         add_rms_norm(x, None, w[0], EPS, tiled=True, h=torch.empty_like(x))
     with pytest.raises(ValueError, match="h must be"):
         add_rms_norm(x, None, w[0], EPS, tiled=True, h=Tiled.empty(8, 64, torch.float16, torch.device(DEVICE)))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shapes_through_every_epilogue(seed: int) -> None:
+    # Seeded sizes that reach the planner's other shapes (one-wave workgroups, several K
+    # chunks per workgroup, uneven K splits): rows 1..200, N a multiple of 32, K of 32.
+    g = torch.Generator().manual_seed(1000 + seed)
+    m = int(torch.randint(1, 201, (1,), generator=g))
+    n = 32 * int(torch.randint(1, 65, (1,), generator=g))
+    k = 32 * int(torch.randint(1, 97, (1,), generator=g))
+    dtype = DTYPES[seed % 2]
+    x, w = operands(m, n, k, dtype, seed=seed)
+    ref, order = linear32(x, w)
+    plans = {e: rows_plan(m, n, k, e) for e in (ROWS_STORE, ROWS_PARTIAL)}
+    print(f"[random] m={m} n={n} k={k} {dtype} plans={plans}")
+    got = rows_linear(x if seed % 3 else Tiled.from_dense(x), w)
+    assert bool(((got.float() - ref).abs() <= ULP[dtype] / 2 * ref.abs() + order + 1e-30).all())
+    part, ks = rows_linear_partials(Tiled.from_dense(x) if seed % 3 else x, w)
+    assert bool(((part.sum(0) - ref).abs() <= order + 1e-30).all())
+    # The SiLU epilogue on [gate; up] = the first and second half of w's rows.
+    half = n // 2
+    if half % 32 == 0:
+        act = rows_silu_gate_up(Tiled.from_dense(x), w).to_dense().float()
+        gate, up = ref[:, :half], ref[:, half:]
+        want = F.silu(gate.to(dtype).float()).to(dtype).float() * up.to(dtype).float()
+        slack = ULP[dtype] * up.abs() * (3.5 * gate.abs() + 1.0) + 2 * (order[:, :half] + order[:, half:])
+        assert bool(((act - want).abs() <= ULP[dtype] / 2 * want.abs() + slack + 1e-30).all())
