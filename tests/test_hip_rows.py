@@ -211,3 +211,30 @@ def test_random_shapes_through_every_epilogue(seed: int) -> None:
         want = F.silu(gate.to(dtype).float()).to(dtype).float() * up.to(dtype).float()
         slack = ULP[dtype] * up.abs() * (3.5 * gate.abs() + 1.0) + 2 * (order[:, :half] + order[:, half:])
         assert bool(((act - want).abs() <= ULP[dtype] / 2 * want.abs() + slack + 1e-30).all())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(8))
+def test_add_rms_norm_random_widths_and_partial_counts(seed: int) -> None:
+    # Widths up to 4096 (8 chunks of 8 per lane) and up to 16 partials: the partial loads
+    # then take several groups; the result stays the ordered sum and rms_norm_rows.
+    g = torch.Generator().manual_seed(2000 + seed)
+    m = int(torch.randint(1, 150, (1,), generator=g))
+    n = 32 * int(torch.randint(1, 129, (1,), generator=g))
+    ks = int(torch.randint(0, 17, (1,), generator=g))
+    dtype = DTYPES[seed % 2]
+    x0 = (torch.randn(m, n, generator=g) * 2).to(dtype).to(DEVICE)
+    w = torch.randn(n, generator=g).to(dtype).to(DEVICE)
+    part = torch.randn(ks, m, n, generator=g).to(DEVICE) if ks else None
+    x = x0.clone()
+    h = add_rms_norm(x, part, w, EPS, tiled=bool(seed % 2))
+    want_x = x0
+    if ks:
+        s = part[0].clone()
+        for z in range(1, ks):
+            s += part[z]
+        want_x = (s + x0.float()).to(dtype)
+    print(f"[add_rms random] m={m} n={n} ks={ks} {dtype}")
+    assert torch.equal(x, want_x)
+    dense = h.to_dense() if seed % 2 else h
+    assert torch.equal(dense, rms_norm_rows(want_x, w, EPS))
