@@ -138,10 +138,10 @@ def test_add_rms_norm_is_the_residual_add_then_rms_norm_rows(m: int, n: int, ks:
         s = part[0].clone()
         for z in range(1, ks):
             s += part[z]
-        want_x = (s + x0.float()).to(dtype)
+        want_x = (s.to(dtype).float() + x0.float()).to(dtype)
     else:
         want_x = x0
-    assert torch.equal(x, want_x), "the residual add: sum of partials in order, plus x, rounded once"
+    assert torch.equal(x, want_x), "the residual add: sum of partials in order rounded, plus x, rounded (model.py:172,179)"
     dense = h.to_dense() if tiled else h
     assert torch.equal(dense, rms_norm_rows(want_x, w, EPS)), "RMSNorm as rms_norm_rows computes it"
     if tiled:
@@ -233,7 +233,7 @@ def test_add_rms_norm_random_widths_and_partial_counts(seed: int) -> None:
         s = part[0].clone()
         for z in range(1, ks):
             s += part[z]
-        want_x = (s + x0.float()).to(dtype)
+        want_x = (s.to(dtype).float() + x0.float()).to(dtype)
     print(f"[add_rms random] m={m} n={n} ks={ks} {dtype}")
     assert torch.equal(x, want_x)
     dense = h.to_dense() if seed % 2 else h

@@ -7,7 +7,8 @@
 // h = rms_norm(x); [gate | up] = F.linear(h, W_gate_up); x = x + F.linear(silu(gate) * up,
 // W_down). No reference kernel corresponds to these launches: they restate those PyTorch
 // calls, with their roundings (each F.linear rounds its fp32 sums to the model dtype
-// once; the residual add rounds once; F.silu rounds, then the product with up rounds).
+// once; the residual add rounds the projection, then the sum; F.silu rounds, then the
+// product with up rounds).
 //
 // rows_gemm. A decode step's projection is an HBM stream of W (2 bytes per weight, a
 // few MB) against a few KB of x per row: the time is the stream's latency and rate, not
@@ -35,8 +36,9 @@
 // gate tile and the matching up tile, and writes act = silu(gate) * up operand-tiled
 // [Mpad, N] (the down projection's x).
 //
-// add_rms_norm. One wave per row: v = x + sum of the KS partials (fixed order) rounded to
-// T is the new residual stream (written back in place), and h = RMSNorm(v) * w, rounded
+// add_rms_norm. One wave per row: v = round_T(x + round_T(sum of the KS partials, fixed
+// order)) is the new residual stream (written back in place; x and xo may alias, since
+// each element is loaded before it is stored), and h = RMSNorm(v) * w, rounded
 // as rms_norm_rows rounds it, is written row-major or operand-tiled.
 #include <cstdlib>
 
@@ -332,7 +334,7 @@ static int dispatch_rows(const RowsArgs& a, const RowsPlan& p, bool xt, hipStrea
 // ---- add_rms_norm -----------------------------------------------------------------------
 // One wave per row; lane l holds 8-element chunks l, l + 64, ... (CPL of them).
 template <typename T, int CPL>
-__global__ __launch_bounds__(64) void add_rms_norm_kernel(const T* __restrict__ x, const float* __restrict__ part,
+__global__ __launch_bounds__(64) void add_rms_norm_kernel(const T* x, const float* __restrict__ part,
                                                            int ks, const T* __restrict__ w, T* xo,
                                                            T* __restrict__ h, bool h_tiled, int M, int rows,
                                                            int N, int64_t xs, int64_t xos, int64_t hs,
@@ -361,8 +363,8 @@ __global__ __launch_bounds__(64) void add_rms_norm_kernel(const T* __restrict__ 
     }
   }
   if (ks > 0) {
-    // The residual stream: x + (sum of the projection's partials in z order), rounded
-    // once. The partials are loaded ZG at a time, every load of a group issued before the
+    // The residual stream as model.py:172,179 computes it: the projection (the sum of
+    // its partials in z order) is rounded to T, then x + it is rounded again. The partials are loaded ZG at a time, every load of a group issued before the
     // first add (ZG * CPL * 8 floats of registers): one round trip per group instead of
     // one per partial.
     constexpr int ZG = 16 / CPL > 0 ? 16 / CPL : 1;
@@ -406,7 +408,8 @@ __global__ __launch_bounds__(64) void add_rms_norm_kernel(const T* __restrict__ 
       const int i = (k * kWave + lane) * 8;
       if (i >= N) continue;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) xv[k].v[e] = from_f32<T>(s[k][e] + to_f32(xv[k].v[e]));
+      for (int e = 0; e < 8; ++e)
+        xv[k].v[e] = from_f32<T>(to_f32(from_f32<T>(s[k][e])) + to_f32(xv[k].v[e]));
       store16(xo + row * xos + i, xv[k]);
     }
   }

@@ -20,7 +20,7 @@ then the final norm (adding the last layer's down partials) and the tied output 
 (model.py:214-221). Other dtypes and larger row counts (a mixed prefill step) take the
 projections through library GEMMs instead:
 
-    h = rms_norm_rows(x); qkv = h @ W_qkv^T; ...; x += attn @ W_o^T (addmm, in place);
+    h = rms_norm_rows(x); qkv = h @ W_qkv^T; ...; x += attn @ W_o^T (rounded, then added in place);
     h = rms_norm_rows(x); x += (silu(gate) * up) @ W_down^T
 
 Weights are random (no checkpoints here): linear weights ~ N(0, 0.02) in the model dtype,
@@ -40,7 +40,7 @@ import torch.nn.functional as F
 from collections.abc import Callable
 
 from tinyserve_amd import hip_attention, hip_fused, hip_prefill, hip_rows
-from tinyserve_amd.step_inputs import Batch, DecodeInputs
+from tinyserve_amd.step_inputs import Batch, DecodeInputs, host_ints
 
 HEAD_MIN_ROWS = 8  # the output head runs on at least this many rows (model.py:64)
 ROWS_MAX = 256  # steps of more rows take the projections through library GEMMs
@@ -171,13 +171,12 @@ class DecodeStep:
             w[p + "self_attn.k_norm.weight"], cos, sin, slots, self.pool.k[i],
             self.pool.v[i], s.rms_norm_eps)  # fmt: skip
         attn = attend(i, q)
-        # Residual adds ride in the GEMMs (beta = 1), in place: x is this step's own
-        # activation, and an out-of-place addmm would first copy x into a new output (one
-        # more launch per add).
-        x.addmm_(attn.reshape(n, s.q_size), w[p + "self_attn.o_proj.weight"].t())
+        # Residual adds as model.py:172,179 writes them: the projection is rounded to the
+        # model dtype, then the sum (in place: x is this step's own activation).
+        x.add_(F.linear(attn.reshape(n, s.q_size), w[p + "self_attn.o_proj.weight"]))
         h = hip_fused.rms_norm_rows(x, w[p + "post_attention_layernorm.weight"], s.rms_norm_eps)
         gate, up = F.linear(h, w[p + "mlp.gate_up_proj.weight"]).chunk(2, dim=1)
-        return x.addmm_(F.silu(gate) * up, w[p + "mlp.down_proj.weight"].t())
+        return x.add_(F.linear(F.silu(gate) * up, w[p + "mlp.down_proj.weight"]))
 
     def _layers_rows(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, slots: torch.Tensor,
                      attend: Callable[[int, torch.Tensor], torch.Tensor]) -> torch.Tensor:  # fmt: skip
@@ -245,14 +244,14 @@ class DecodeStep:
         scale, bs = self.scale, self.pool.block_size
 
         def ints(xs: list[int]) -> torch.Tensor:
-            return torch.tensor(xs, dtype=torch.int32, device=dev)
+            return host_ints(xs, torch.int32, dev)
 
         if one:
-            d_idx = torch.tensor(one, device=dev)
-            d_rows = torch.tensor([starts[b] for b in one], device=dev)
+            d_idx = host_ints(one, torch.int64, dev)
+            d_rows = host_ints([starts[b] for b in one], torch.int64, dev)
             d_tables, d_lens = batch.block_tables[d_idx], batch.context_lens[d_idx]
         if rest:
-            p_idx = torch.tensor(rest, device=dev)
+            p_idx = host_ints(rest, torch.int64, dev)
             p_starts, p_qlens = ints([starts[b] for b in rest]), ints([qlens[b] for b in rest])
             p_tables, p_lens = batch.block_tables[p_idx], batch.context_lens[p_idx]
             max_q = max(qlens[b] for b in rest)

@@ -160,8 +160,10 @@ def rows_linear_partials(x: torch.Tensor | Tiled, w: torch.Tensor,
     if partial is not None and (partial.dtype != torch.float32 or not partial.is_contiguous()
                                 or _lib.require_device(partial) != dev):  # fmt: skip
         raise ValueError("partial must be a contiguous float32 buffer on x's device")
-    if partial is None or partial.numel() < ks * m * n:
+    if partial is None:
         partial = torch.empty(ks * m * n, dtype=torch.float32, device=w.device)
+    elif partial.numel() < ks * m * n:
+        raise ValueError(f"partial holds {partial.numel()} floats; this projection needs {ks * m * n}")
     _lib.call("ts_rows_gemm", xp, xt, xs, w.data_ptr(), w.stride(0), None, 0, partial.data_ptr(),
               partial.numel(), m, n, k, ROWS_PARTIAL, _lib.dtype_code(w), _lib.stream_of(dev))  # fmt: skip
     return partial.view(-1)[: ks * m * n].view(ks, m, n), ks
