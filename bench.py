@@ -46,22 +46,26 @@ HQ, HKV, D, BS = 16, 8, 128, 16
 
 
 def decode_bytes(b: int, ctx: int, splits: int = 1, esize: int = 2) -> dict[str, int]:
-    """Algorithmic bytes of one step, and of its attention kernel alone (which writes the
-    output itself with one split, fp32 partials for the combine otherwise)."""
+    """Algorithmic bytes of one step, and of its attention kernel alone (the same: the
+    launcher's one launch, with one split or the splits merged in each workgroup, writes
+    the output itself)."""
     kv = b * ctx * HKV * D * 2 * esize
     q_io = 2 * b * HQ * D * esize
     tables = b * math.ceil(ctx / BS) * 4
     lens = b * 4
     step = kv + q_io + tables + lens
-    return {"step": step, "split_kernel": step if splits == 1 else step - q_io // 2}
+    return {"step": step, "split_kernel": step}
 
 
 def split_kernel_launch(c, splits: int, m, l, acc, out, stream: int) -> None:
-    """The split kernel alone, exactly as hip_attention launches it."""
+    """The split kernel alone, as hip_attention launches it: with ``m`` None and splits > 1
+    the split ranges' states merge in each workgroup (one launch, output written);
+    with partial buffers, the HBM-partials kernel that ``combine_launch`` finishes."""
     q, k = c.q, c.k_cache
+    ptrs = (None, None, None) if m is None else (m.data_ptr(), l.data_ptr(), acc.data_ptr())
     _lib.call("ts_decode_split", q.data_ptr(), k.data_ptr(), c.v_cache.data_ptr(),
               c.block_tables.data_ptr(), c.context_lens.data_ptr(), out.data_ptr(),
-              m.data_ptr(), l.data_ptr(), acc.data_ptr(), q.shape[0], HQ, HKV, D, BS,
+              *ptrs, q.shape[0], HQ, HKV, D, BS,
               q.stride(0), q.stride(1), out.stride(0), out.stride(1), k.stride(0), k.stride(1),
               c.block_tables.stride(0), c.block_tables.shape[1], splits, 0, c.scale, 1, stream)  # fmt: skip
 
@@ -77,14 +81,9 @@ def time_decode(batch: int, ctx: int, splits: int, steps: int, warmup: int) -> d
     stream = torch.cuda.current_stream(dev)
     s = stream.cuda_stream
     out = torch.empty_like(c.q)
-    m = torch.empty((batch, HQ, splits), dtype=torch.float32, device=dev)
-    l = torch.empty_like(m)  # noqa: E741
-    acc = torch.empty((batch, HQ, splits, D), dtype=torch.float32, device=dev)
 
-    def step() -> None:
-        split_kernel_launch(c, splits, m, l, acc, out, s)
-        if splits > 1:
-            combine_launch(splits, m, l, acc, out, s)
+    def step() -> None:  # one launch: the split ranges (if any) merge in each workgroup
+        split_kernel_launch(c, splits, None, None, None, out, s)
 
     for _ in range(warmup):
         step()
@@ -101,17 +100,7 @@ def time_decode(batch: int, ctx: int, splits: int, steps: int, warmup: int) -> d
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_start.elapsed_time(t_end)
-    if splits == 1:
-        split_ms = total_ms / steps  # the step is the attention kernel alone
-    else:
-        # The attention kernel alone, `steps` back-to-back launches on the same stream.
-        t_start.record(stream)
-        for _ in range(steps):
-            split_kernel_launch(c, splits, m, l, acc, out, s)
-        t_end.record(stream)
-        torch.cuda.synchronize()
-        split_ms = t_start.elapsed_time(t_end) / steps
-        combine_launch(splits, m, l, acc, out, s)
+    split_ms = total_ms / steps  # the step is the attention kernel alone
     # The public entry point gives the same result (a check, outside the timed region).
     ref_out = launch_paged_decode_split(*c.args(), c.scale, BS, num_splits=splits)
     assert torch.equal(ref_out, out), "bench launch differs from the entry point"
@@ -275,9 +264,10 @@ def batched_sdpa_prefill(p, out: torch.Tensor) -> torch.Tensor:
 def extra_measurements() -> dict:
     dev = torch.device("cuda:0")
     res: dict = {}
-    # Config 2: decode B=32 x 256, a 4096-block pool: 4 splits + combine as the config
-    # states (fp32 partials in HBM and a second launch), and the policy's single launch
-    # (each sequence split over the waves of a workgroup, merged in LDS).
+    # Config 2: decode B=32 x 256, a 4096-block pool: 4 splits as the config states, through
+    # the launcher (the four ranges' states merged in each workgroup's LDS, one launch),
+    # and the policy's single launch (each sequence split over the waves of a workgroup);
+    # then the same 4 splits as fp32 partials in HBM and the combine launch.
     c = decode_bench_case(32, 256, pool_blocks=4096, device=dev, seed=1)
     nb = decode_bytes(32, 256)["step"]
     outs = {}
@@ -287,14 +277,29 @@ def extra_measurements() -> dict:
             launch_paged_decode_split(*c.args(), c.scale, BS, num_splits=splits)
 
         ms, ms_g = loop_ms(call, 200, 20), graph_ms(call)
-        plan = decode_plan(32, HQ, HKV, D, BS, c.block_tables.shape[1], splits or 1)
+        plan = decode_plan(32, HQ, HKV, D, BS, c.block_tables.shape[1], 1)  # in-group splits: the one-split grid
         res[key] = {"us": round(ms * 1e3, 2), "GB/s": round(nb / ms / 1e6, 1),
                     "graph_us": round(ms_g * 1e3, 2), "graph_GB/s": round(nb / ms_g / 1e6, 1),
-                    "launches": "split kernel + combine" if splits else "one launch",
+                    "launches": "one launch, 4 range states merged in LDS" if splits else "one launch",
                     "kernel": kernel_name(plan), "grid": plan["grid"],
                     "waves_per_group": plan["waves_per_group"]}  # fmt: skip
     res["decode_b32_ctx256_policy"]["max_abs_vs_s4"] = check(
         outs["decode_b32_ctx256_policy"], outs["decode_b32_ctx256_s4"], 4e-3, "config 2: policy vs 4 splits")
+    hout = torch.empty_like(c.q)
+    m = torch.empty((32, HQ, 4), dtype=torch.float32, device=dev)
+    l = torch.empty_like(m)  # noqa: E741
+    acc = torch.empty((32, HQ, 4, D), dtype=torch.float32, device=dev)
+
+    def hbm() -> None:
+        s = torch.cuda.current_stream(dev).cuda_stream  # a graph capture runs on its own stream
+        split_kernel_launch(c, 4, m, l, acc, hout, s)
+        combine_launch(4, m, l, acc, hout, s)
+
+    ms, ms_g = loop_ms(hbm, 200, 20), graph_ms(hbm)
+    res["decode_b32_ctx256_s4_hbm_partials"] = {
+        "us": round(ms * 1e3, 2), "GB/s": round(nb / ms / 1e6, 1), "graph_us": round(ms_g * 1e3, 2),
+        "graph_GB/s": round(nb / ms_g / 1e6, 1), "launches": "split kernel (fp32 partials) + combine",
+        "max_abs_vs_s4": check(hout, outs["decode_b32_ctx256_s4"], 4e-3, "config 2: HBM partials vs in-group")}  # fmt: skip
     # The reference's own published decode shapes (fp16, one layer, Qwen3 heads; its T4
     # timings in BASELINE.md): B=32 x 1024, B=32 x 160, B=64 x 1024, the policy's launch.
     for b, ctx in ((32, 1024), (32, 160), (64, 1024)):
@@ -484,13 +489,13 @@ def main() -> None:
         print(json.dumps({"profile": args.profile, "launches": 3, "sequences": len(lens),
                           **calibration_copies(args.copy_mb)}), flush=True)  # fmt: skip
         return
-    if args.profile == "decode_b32_ctx256":  # config 2: 4 splits + combine, then the policy's launch
+    if args.profile == "decode_b32_ctx256":  # config 2: 4 splits, then the policy's launch
         c = decode_bench_case(32, 256, pool_blocks=4096, device=torch.device("cuda:0"), seed=1)
         for splits in (4, None):
             for _ in range(20):
                 launch_paged_decode_split(*c.args(), c.scale, BS, num_splits=splits)
         torch.cuda.synchronize()
-        print(json.dumps({"profile": args.profile, "launches": "20 x (split kernel + combine), then 20 x one launch",
+        print(json.dumps({"profile": args.profile, "launches": "20 x 4 splits through the launcher (one launch, range states merged in LDS), then 20 x the policy's launch",
                           **calibration_copies(args.copy_mb)}), flush=True)  # fmt: skip
         return
     if args.profile == "step_projections":  # config 5's four projections of a layer, W cold
@@ -537,7 +542,7 @@ def main() -> None:
         "config": {"workload": f"paged decode attention, one layer, B={args.batch} x ctx={args.ctx}, "
                                f"16 q / 8 kv heads, head_dim 128, block 16, "
                                + ("one launch (in-workgroup split-K)" if splits == 1
-                                  else f"split-K {splits} + combine"),
+                                  else f"split-K {splits}, range states merged in LDS (one launch)"),
                    "batch": args.batch, "ctx": args.ctx, "splits": splits,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": kernel_name(plan), "kernel_source": "ts_decode_plan",

@@ -68,10 +68,16 @@ const char* ts_strerror(int code);
  * Sequence b's blocks 0 .. ceil(lens[b] / block_size) - 1 are cut into `splits`
  * contiguous ranges of ceil(nblocks / splits) blocks (the reference's ranges,
  * triton_attention.py:283-286). splits == 1: `out` [B, Hq, D] receives the normalised
- * result in the q dtype and m/l/acc are not touched (may be NULL). splits > 1: every range
- * writes its fp32 partial to m, l [B, Hq, splits] and acc [B, Hq, splits, D]
- * (contiguous, part index (b * Hq + h) * splits + split); `out` is not touched, and
- * ts_decode_combine finishes the result. m is stored in base-2 units (log2 e * max score).
+ * result in the q dtype and m/l/acc are not touched (may be NULL). splits > 1 with m, l
+ * and acc all NULL: each (sequence, head tile) workgroup keeps every range's softmax state
+ * in LDS, merges them by ts_decode_combine's rule and writes `out` (one launch, the
+ * combine of _merge_splits_kernel, :299-327, included); TS_EUNSUPPORTED, before any
+ * launch, if block_size is smaller than the tokens one loop iteration streams (16 at
+ * fp16 D=128) or the states exceed 64 KiB of LDS, and the caller then takes the path
+ * below. splits > 1 with m, l, acc: every range writes its fp32 partial to
+ * m, l [B, Hq, splits] and acc [B, Hq, splits, D] (contiguous, part index
+ * (b * Hq + h) * splits + split); `out` is not touched, and ts_decode_combine finishes the
+ * result. m is stored in base-2 units (log2 e * max score).
  *
  * max_blocks: the width of block_tables (entries per row the caller filled, so every
  * context is at most max_blocks * block_size), or 0 if unknown. It only picks how the

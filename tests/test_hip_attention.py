@@ -194,11 +194,31 @@ def test_benchmark_sized_batch() -> None:
     check(decode_case([193] * 64, dtype=torch.float16, seed=1))
 
 
+def hbm_split_combine(g: DecodeCase, splits: int) -> torch.Tensor:
+    """The reference's two launches exactly: every split range writes its fp32 partial
+    (m, l, acc) to HBM, then the combine kernel merges them."""
+    b, hq, d = g.q.shape
+    out = torch.empty_like(g.q)
+    m = torch.empty((b, hq, splits), dtype=torch.float32, device=DEVICE)
+    l = torch.empty_like(m)  # noqa: E741
+    acc = torch.empty((b, hq, splits, d), dtype=torch.float32, device=DEVICE)
+    dt, stream = _lib.dtype_code(g.q), _lib.stream_of(0)
+    _lib.call("ts_decode_split", g.q.data_ptr(), g.k_cache.data_ptr(), g.v_cache.data_ptr(),
+              g.block_tables.data_ptr(), g.context_lens.data_ptr(), None, m.data_ptr(), l.data_ptr(),
+              acc.data_ptr(), b, hq, g.k_cache.shape[1], d, g.block_size, g.q.stride(0), g.q.stride(1),
+              0, 0, g.k_cache.stride(0), g.k_cache.stride(1), g.block_tables.stride(0),
+              g.block_tables.shape[1], splits, 0, g.scale, dt, stream)  # fmt: skip
+    _lib.call("ts_decode_combine", m.data_ptr(), l.data_ptr(), acc.data_ptr(), out.data_ptr(),
+              b, hq, d, out.stride(0), out.stride(1), splits, dt, stream)  # fmt: skip
+    return out
+
+
 def test_baseline_config_2() -> None:
-    # fp16, B=32 at context 256, a 4096-block pool, 4 splits + combine
-    # (the reference's ranges of ceil(16 / 4) = 4 blocks each write fp32 partials, and the
-    # combine pass finishes); and the policy's one launch (no count given), which splits
-    # each sequence over the waves of a workgroup instead.
+    # BASELINE config 2: fp16, B=32 at context 256, a 4096-block pool, 4 splits: the
+    # reference's ranges of ceil(16 / 4) = 4 blocks, each with its own softmax state, merged
+    # in each workgroup's LDS (the launcher's path), and the same four states as fp32
+    # partials in HBM merged by the combine pass; and the policy's one launch (no count
+    # given), which splits each sequence over the waves of a workgroup.
     c = decode_case([256] * 32, dtype=torch.float16, pool_blocks=4096, seed=0)
     want = oracle32(c)
     g = on_gpu(c)
@@ -206,9 +226,45 @@ def test_baseline_config_2() -> None:
     assert plan["grid"][2] == 4, plan
     out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, num_splits=4)
     assert torch.isfinite(out).all()
-    assert_contract(out, want, torch.float16, "config 2, 4 splits + combine")
+    assert_contract(out, want, torch.float16, "config 2, 4 splits merged in the workgroup")
+    hbm = hbm_split_combine(g, 4)
+    assert_contract(hbm, want, torch.float16, "config 2, 4 splits + combine")
+    torch.testing.assert_close(out, hbm, atol=1e-3, rtol=0)
     policy = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size)
     assert_contract(policy, want, torch.float16, "config 2, policy (one launch)")
+
+
+@pytest.mark.parametrize("case", [
+    # (lens, heads, dtype, block_size): one-wave workgroups (512 sequences), 2-8 wave
+    # workgroups, length pairs (33-64 sequences, odd and even), the heavy budget (few long
+    # sequences), four query heads per wave, bf16 and fp32, more splits than blocks.
+    ([1 + (97 * i) % 400 for i in range(512)], (16, 8), torch.float16, 16),
+    ([256] * 32, (16, 8), torch.float16, 16),
+    ([1 + (389 * i) % 1000 for i in range(45)], (16, 8), torch.float16, 16),
+    ([1 + (389 * i) % 3000 for i in range(64)], (16, 8), torch.bfloat16, 16),
+    ([4096, 1, 2500, 17], (16, 8), torch.float16, 16),
+    ([300, 17, 64, 1000, 5], (32, 8), torch.float16, 16),
+    ([300, 17, 64, 1000, 5], (16, 8), torch.float32, 16),
+    ([1, 2, 17, 33], (16, 8), torch.float16, 16),
+    ([700, 31, 1200], (16, 8), torch.float16, 32),
+])  # fmt: skip
+@pytest.mark.parametrize("splits", [2, 3, 4, 7, 16])
+def test_in_workgroup_splits_match_the_hbm_partials(case: tuple, splits: int) -> None:
+    # An explicit split count merges the ranges' states in LDS (one launch); the same
+    # ranges as HBM partials + the combine launch must give the same output up to fp32
+    # summation order, and both the oracle's.
+    lens, (hq, hkv), dtype, bs = case
+    c = decode_case(lens, hq, hkv, dtype=dtype, block_size=bs, seed=len(lens) + splits)
+    g = on_gpu(c)
+    out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, num_splits=splits)
+    hbm = hbm_split_combine(g, splits)
+    assert torch.isfinite(out).all()
+    tol = {torch.float32: 2e-6, torch.float16: 1e-3, torch.bfloat16: 8e-3}[dtype]
+    torch.testing.assert_close(out.float(), hbm.float(), atol=tol, rtol=0)
+    rows = list(range(0, len(lens), max(1, len(lens) // 16)))
+    sub = DecodeCase(c.q[rows], c.k_cache, c.v_cache, c.block_tables[rows], c.context_lens[rows],
+                     c.scale, c.block_size)  # fmt: skip
+    assert_matches(out[rows], oracle32(sub), dtype, f"{len(lens)} sequences, {splits} splits")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])

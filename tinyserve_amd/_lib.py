@@ -108,6 +108,21 @@ def call(name: str, *args: object) -> None:
         raise RuntimeError(f"{name}: HIP error {rc}: {msg}")
 
 
+def call_status(name: str, *args: object) -> int:
+    """Call entry point ``name`` and return its status; raise only on a HIP error (a
+    positive status), so the caller can take another path on a TS_E* code."""
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load(), name)
+    rc = fn(*args)
+    if rc > 0:
+        raise RuntimeError(f"{name}: HIP error {rc}: {load().ts_strerror(rc).decode()}")
+    return rc
+
+
+TS_EUNSUPPORTED = -2
+
+
 def dtype_code(t: torch.Tensor) -> int:
     try:
         return DTYPES[t.dtype]

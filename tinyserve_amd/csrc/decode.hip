@@ -36,6 +36,7 @@
 // cross-lane work except the LPT-lane dot-product reduction. The token lanes are
 // merged once at the end with the two-partial rule m = max(m1, m2),
 // l = 2^(m1-m) l1 + 2^(m2-m) l2 (same for acc), the rule the combine pass uses too.
+#include <algorithm>
 #include <mutex>
 
 #include "common.h"
@@ -95,6 +96,12 @@ struct AttendArgs {
   int64_t q_sb, q_sh, o_sb, o_sh, k_ss, k_sh, bt_s;
   float scale_log2;  // softmax scale * log2(e)
   int stream_kv;     // decode, light budget: K/V through non-temporal loads
+  // decode, in-workgroup split-K: the walk of each sequence is cut at the block ranges of
+  // `cuts` splits (split s: blocks [s * ceil(n / cuts), ...), the reference's ranges);
+  // every range piece's softmax state is parked in LDS and the workgroup merges them. 0:
+  // no cuts (the workgroup's waves merge one state each).
+  int cuts;
+  int width;  // decode: block-table width when at most 64 (the row is loaded up front), else 0
 };
 
 // Partial dot product of one 16-byte K vector with the matching q vector, fp32 result
@@ -242,7 +249,7 @@ __device__ __forceinline__ void merge_group_waves(const Args& a, const StateSlot
 // states merge to an empty state without inf - inf.
 constexpr float kNoMax = -1.0e30f;
 
-template <typename T, int D, int HT, bool PREFILL, int BUDGET>
+template <typename T, int D, int HT, bool PREFILL, int BUDGET, bool CUT = false>
 __global__ __launch_bounds__(PREFILL ? kWave : kWave * (BudgetOf<BUDGET>::kLightish ? kMaxWavesLight : kMaxWavesPerGroup))
 __attribute__((amdgpu_waves_per_eu(BudgetOf<BUDGET>::kWavesPerEU)))
 void paged_attend_kernel(const AttendArgs a) {
@@ -266,6 +273,10 @@ void paged_attend_kernel(const AttendArgs a) {
   // Length pairs: the two sequences, and this wave's segments (sequence, block range).
   int pair_a = -1, pair_b = -1, len_a = 0, len_b = 0, n_a = 0, share = 1, nseg = 1;
   int seg_seq[2] = {0, 0}, seg_first[2] = {0, 0}, seg_last[2] = {0, 0};
+  // Decode, a narrow table (at most 64 blocks) and no pairs: the sequence's whole row is
+  // loaded first, one entry per lane, in parallel with its context length instead of
+  // after it.
+  int win_pre = 0;
   if constexpr (PREFILL) {
     seq = blockIdx.x / a.max_q_len;
     const int i = blockIdx.x - seq * a.max_q_len;
@@ -277,6 +288,7 @@ void paged_attend_kernel(const AttendArgs a) {
     orow = row * a.o_sb;
   } else {
     seq = blockIdx.y;
+    if (!a.by_length && a.width > 0) win_pre = lane < a.width ? a.bt[seq * a.bt_s + lane] : 0;
     if (a.by_length) {
       // Workgroup y takes the sequences ranked y and B - 1 - y by length (longest
       // first, ties by index): lane b ranks sequence b against the others (B <= 64).
@@ -345,9 +357,26 @@ void paged_attend_kernel(const AttendArgs a) {
   if constexpr (!PREFILL) pair = a.by_length;
   if (!pair) seg_seq[0] = seq, seg_first[0] = first, seg_last[0] = last;
 
+  // Cut mode: a wave's walk of one sequence is cut at every multiple of that sequence's
+  // split length pc = ceil(n / cuts) blocks into pieces, each with its own softmax state
+  // parked in LDS. The piece of split k walked by wave w takes slot k + w (+ cuts + W for
+  // the second sequence of a length pair): along a sequence's blocks both k and w only
+  // grow, and at least one of them grows from one piece to the next, so slots never
+  // collide. Slots no piece takes hold an empty state (m = -1e30, l = 0, acc = 0, which
+  // weighs 0), written before the walk; the merge takes every slot of a sequence in slot
+  // order (position order, so the result does not depend on timing).
   TokenState<T, D, HT, LB> st;
   extern __shared__ float lds_slots[];
-  const StateSlots<HT, D> ss{lds_slots, (pair ? 2 : 1) * (PREFILL ? 1 : a.wpg)};
+  const StateSlots<HT, D> ss{lds_slots, CUT ? (pair ? 2 : 1) * (a.cuts + nw)
+                                            : (pair ? 2 : 1) * (PREFILL ? 1 : a.wpg)};
+  if constexpr (CUT) {
+    for (int i = threadIdx.x; i < ss.ns * HT; i += nw * kWave) {
+      lds_slots[i] = kNoMax;           // m
+      lds_slots[ss.ns * HT + i] = 0.f;  // l
+    }
+    for (int i = threadIdx.x; i < ss.ns * HT * D; i += nw * kWave) lds_slots[2 * ss.ns * HT + i] = 0.f;
+    __syncthreads();
+  }
   for (int sgi = 0; sgi < nseg; ++sgi) {
   if (pair) {
     seq = seg_seq[sgi];
@@ -356,6 +385,18 @@ void paged_attend_kernel(const AttendArgs a) {
     first = seg_first[sgi];
     last = seg_last[sgi];
   }
+  // Cut mode: this segment's first slot, and the next split boundary (tokens); set once
+  // the segment's first loads are in flight.
+  const int cut_seq = pair && seq != pair_a ? 1 : 0;
+  int slot = 0, next_cut = 0x7fffffff, pc_tokens = 0;
+  auto cut_setup = [&]() {
+    const int n = (ctx + bs_mask) >> lbs;
+    const int pc = __builtin_amdgcn_readfirstlane(max(1, (n + a.cuts - 1) / a.cuts));
+    const int k = __builtin_amdgcn_readfirstlane(first / pc);
+    slot = cut_seq * (a.cuts + nw) + k + wave;
+    pc_tokens = pc << lbs;
+    next_cut = (k + 1) * pc_tokens;
+  };
   const T* qp = static_cast<const T*>(a.q) + qrow;
   Pack16<T> qv[HT][NV];
 #pragma unroll
@@ -381,7 +422,13 @@ void paged_attend_kernel(const AttendArgs a) {
     // the positions pass its end. An iteration never straddles two windows (it covers
     // TPW <= 64 positions starting at a multiple of TPW from a window start).
     int chunk = first;
-    int win = (chunk + lane < last) ? btrow[chunk + lane] : 0;
+    int win;
+    if (!pair && a.width > 0) {
+      chunk = 0;  // the whole row (at most 64 blocks) is in win_pre
+      win = win_pre;
+    } else {
+      win = (chunk + lane < last) ? btrow[chunk + lane] : 0;
+    }
 
     // NBUF iterations in flight: the loads of iteration i + NBUF - 1 are issued before
     // iteration i's math (ring of NBUF register buffers, indices fixed by unrolling).
@@ -451,6 +498,7 @@ void paged_attend_kernel(const AttendArgs a) {
 #pragma unroll
     for (int j = 0; j + 1 < NBUF; ++j)
       if (t0 + j * TPW < t1) issue(kb[j], vb[j], t0 + j * TPW);
+    if constexpr (CUT) cut_setup();
     for (int base = t0; base < t1; base += NBUF * TPW) {
 #pragma unroll
       for (int j = 0; j < NBUF; ++j) {
@@ -459,13 +507,58 @@ void paged_attend_kernel(const AttendArgs a) {
         const int pn = p0 + (NBUF - 1) * TPW;
         if (pn < t1) issue(kb[(j + NBUF - 1) % NBUF], vb[(j + NBUF - 1) % NBUF], pn);
         attend(kb[j], vb[j], p0);
+        if constexpr (CUT) {
+          // A split boundary (a whole number of iterations past t0: the host runs cut
+          // mode only when TPW divides the block size): park this piece, start the next.
+          if (p0 + TPW == next_cut && next_cut < t1) {
+            merge_token_lanes(st);
+            park_state(ss, st, slot++, tl == 0 ? c : -1);
+#pragma unroll
+            for (int g = 0; g < HT; ++g) {
+              st.m[g] = kNoMax;
+              st.l[g] = 0.f;
+#pragma unroll
+              for (int e = 0; e < E; ++e) st.acc[g][e] = 0.f;
+            }
+            next_cut += pc_tokens;
+          }
+        }
       }
     }
   }
 
   merge_token_lanes(st);
-  if (pair) park_state(ss, st, 2 * wave + sgi, tl == 0 ? c : -1);
+  if constexpr (CUT) {
+    if (first < last) {
+      park_state(ss, st, slot, tl == 0 ? c : -1);
+    }
+  } else {
+    if (pair) park_state(ss, st, 2 * wave + sgi, tl == 0 ? c : -1);
+  }
   }  // segments
+  if constexpr (CUT) {
+    // Every piece of a sequence, in position order, by the two-partial rule: the
+    // sequence's result is the merge of its split ranges' states (each range possibly in
+    // several pieces, merged by the same rule).
+    __syncthreads();
+    const int parts = pair && pair_b >= 0 ? 2 : 1;
+    for (int t = threadIdx.x; t < parts * HT * D; t += nw * kWave) {
+      const int pi = t / (HT * D);
+      const int g = (t % (HT * D)) / D, d = t % D;
+      const int s0 = pi * (a.cuts + nw), s1 = s0 + a.cuts + nw;
+      float mm = kNoMax;
+      for (int s2 = s0; s2 < s1; ++s2) mm = fmaxf(mm, ss.m(s2, g));
+      float den = 0.f, num = 0.f;
+      for (int s2 = s0; s2 < s1; ++s2) {
+        const float f = fast_exp2(ss.m(s2, g) - mm);
+        den = fmaf(f, ss.l(s2, g), den);
+        num = fmaf(f, ss.acc(s2, g, d), num);
+      }
+      const int64_t row = static_cast<int64_t>(pi ? pair_b : (pair ? pair_a : seq)) * a.o_sb;
+      static_cast<T*>(a.out)[row + (h0 + g) * a.o_sh + d] = from_f32<T>(num / den);
+    }
+    return;
+  }
   if constexpr (!PREFILL) {
     if (pair) {
       __syncthreads();
@@ -634,6 +727,25 @@ __global__ __launch_bounds__(64) void combine_kernel(const float* __restrict__ m
 
 template <typename T, int D, int HT, bool PREFILL>
 static int launch_attend(const AttendArgs& a, dim3 grid, bool light, size_t lds, hipStream_t stream) {
+  if constexpr (!PREFILL) {
+    if (a.cuts > 1) {
+      // In-workgroup split-K over the reference's split ranges (cut mode).
+      if constexpr (D == 64 || D == 128) {
+        if (light && a.stream_kv) {
+          hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, false, kLightStream, true>), grid,
+                             dim3(kWave * a.wpg), lds, stream, a);
+          return launch_status();
+        }
+      }
+      if (light)
+        hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, false, kLight, true>), grid,
+                           dim3(kWave * a.wpg), lds, stream, a);
+      else
+        hipLaunchKernelGGL((paged_attend_kernel<T, D, HT, false, kHeavy, true>), grid,
+                           dim3(kWave * a.wpg), lds, stream, a);
+      return launch_status();
+    }
+  }
   {
     if constexpr (!PREFILL && (D == 64 || D == 128)) {
       if (light && a.stream_kv) {
@@ -751,6 +863,17 @@ struct DecodePlan {
   size_t lds;     // dynamic LDS bytes
 };
 
+// Tokens one wave streams per loop iteration (TPW of the kernel's RowShape).
+static int tokens_per_iteration(int dtype, int D, int ht, int budget) {
+  const int lb = budget != kHeavy ? (ht == 4 ? 16 : 32) : 64;
+  const int row = D * (dtype == TS_F32 ? 4 : 2);
+  const int lpt = row <= lb ? 1 : std::min(row / lb, kWave);
+  return kWave / lpt;
+}
+
+// LDS of a cut-mode workgroup: its pieces' states.
+constexpr size_t kMaxInGroupLds = 64 << 10;
+
 static int plan_decode(int B, int Hq, int Hkv, int D, int block_size, int max_blocks, int splits,
                        int head_tile, int dtype, DecodePlan* plan) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || splits < 1 || !is_pow2(block_size))
@@ -839,17 +962,30 @@ extern "C" int ts_decode_split(const void* q, const void* k_cache, const void* v
     return TS_EINVAL;
   if (B == 0) return 0;
   if (B > 65535) return TS_EUNSUPPORTED;  // sequences are the grid's y dimension
-  if (splits > 1 && (!m || !l || !acc)) return TS_EINVAL;
-  if (splits == 1 && !out) return TS_EINVAL;
+  // m, l and acc all null with splits > 1: the split ranges stay inside each workgroup.
+  const bool in_group = splits > 1 && !m && !l && !acc;
+  if (splits > 1 && !in_group && (!m || !l || !acc)) return TS_EINVAL;
+  if ((splits == 1 || in_group) && !out) return TS_EINVAL;
   DecodePlan p;
-  const int rc = plan_decode(B, Hq, Hkv, D, block_size, max_blocks, splits, head_tile, dtype, &p);
+  const int rc = plan_decode(B, Hq, Hkv, D, block_size, max_blocks, in_group ? 1 : splits, head_tile,
+                             dtype, &p);
   if (rc) return rc;
   AttendArgs a{q, k_cache, v_cache, block_tables, context_lens, out, m, l, acc, nullptr,
-               nullptr, Hq, Hq / Hkv, ilog2(block_size), splits, p.wpg, 0, p.by_length, B,
-               q_stride_b, q_stride_h, o_stride_b, o_stride_h, k_stride_slot, k_stride_head,
-               bt_stride, scale * kLog2e, 0};
+               nullptr, Hq, Hq / Hkv, ilog2(block_size), in_group ? 1 : splits, p.wpg, 0,
+               p.by_length, B, q_stride_b, q_stride_h, o_stride_b, o_stride_h, k_stride_slot,
+               k_stride_head, bt_stride, scale * kLog2e, 0};
   a.stream_kv = p.budget == kLightStream ? 1 : 0;
-  return dispatch_attend<false>(a, dtype, D, p.ht, p.grid, p.budget != kHeavy, p.lds,
+  a.width = max_blocks > 0 && max_blocks <= kWave && !p.by_length ? max_blocks : 0;
+  size_t lds = p.lds;
+  if (in_group) {
+    // A piece ends at a split boundary between two loop iterations only if an
+    // iteration's tokens never straddle a block; every piece's state needs an LDS slot.
+    if (block_size % tokens_per_iteration(dtype, D, p.ht, p.budget)) return TS_EUNSUPPORTED;
+    lds = static_cast<size_t>((p.by_length ? 2 : 1) * (splits + p.wpg) * state_slot_bytes(p.ht, D));
+    if (lds > kMaxInGroupLds) return TS_EUNSUPPORTED;
+    a.cuts = splits;
+  }
+  return dispatch_attend<false>(a, dtype, D, p.ht, p.grid, p.budget != kHeavy, lds,
                                 static_cast<hipStream_t>(stream));
 }
 

@@ -8,8 +8,11 @@ Qwen3-0.6B), so every K/V byte is read once; the per-query-head launch
 (``paged_decode_attention``, any head grouping) gives it one query head. Each wave
 streams 16-byte K/V vectors of its range of cache blocks, three iterations in flight, and
 keeps an online softmax per token lane, merged across lanes once at the end. With more
-than one split, every range writes an fp32 partial (m, l, acc) and a second kernel
-combines them (the reference's ``_merge_splits_kernel``, :299-327).
+than one split, each (sequence, head tile) workgroup walks the reference's S block
+ranges, parks each range's softmax state (m, l, acc) in LDS and merges them by the
+reference's merge rule (``_merge_splits_kernel``, :299-327) before one write of the
+output; shapes that cannot (blocks smaller than a loop iteration's tokens, too many
+states for the LDS) write the fp32 partials to HBM and a second kernel combines them.
 
 Every launch goes on torch's current stream, never synchronises and never allocates
 outside torch's caching allocator, so a HIP graph can capture the ``launch_*``
@@ -178,6 +181,18 @@ def _launch(
                   None, None, None, b, hq, hkv, d, block_size, *strides, width, 1, head_tile,
                   scale, dt, stream)  # fmt: skip
         return out
+    # The split ranges inside each workgroup: every range's softmax state is merged with
+    # the others in LDS, and the result written once. Shapes it cannot take (blocks
+    # smaller than a loop iteration's tokens, or more states than its LDS holds) write
+    # fp32 partials to HBM and combine them in a second launch.
+    rc = _lib.call_status("ts_decode_split", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                          block_tables.data_ptr(), context_lens.data_ptr(), out.data_ptr(),
+                          None, None, None, b, hq, hkv, d, block_size, *strides, width, splits,
+                          head_tile, scale, dt, stream)  # fmt: skip
+    if rc == 0:
+        return out
+    if rc != _lib.TS_EUNSUPPORTED:
+        raise ValueError(f"ts_decode_split: {_lib.load().ts_strerror(rc).decode()}")
     m = torch.empty((b, hq, splits), dtype=torch.float32, device=q.device)
     l = torch.empty_like(m)  # noqa: E741
     acc = torch.empty((b, hq, splits, d), dtype=torch.float32, device=q.device)
@@ -300,12 +315,14 @@ def launch_paged_decode_split(
 ) -> torch.Tensor:
     """The split-K launches alone (:534-586): no checks, no host sync.
 
-    An explicit ``num_splits`` S > 1 runs as the reference runs it: S block ranges of
-    ``ceil(blocks / S)`` each write an fp32 partial (m, l, acc), and a second launch
-    combines them. Without one, the count comes from ``num_splits_for(B, Hkv,
-    max_blocks)``, and a policy count up to ``IN_GROUP_SPLITS`` becomes one launch
-    whose workgroups split each sequence over their waves and merge in LDS (the library
-    sizes the workgroup to the grid): no partials, no second launch."""
+    An explicit ``num_splits`` S > 1 computes what the reference computes: S block
+    ranges of ``ceil(blocks / S)``, each with its own softmax state (m, l, acc), merged
+    by the two-partial rule. The states stay in each workgroup's LDS and the merge runs
+    in the same launch (fp32 partials in HBM and a second launch only for shapes that
+    cannot: block sizes under a loop iteration's tokens). Without a count, it comes
+    from ``num_splits_for(B, Hkv, max_blocks)``, and a policy count up to
+    ``IN_GROUP_SPLITS`` becomes one launch whose workgroups split each sequence over
+    their waves (the library sizes the workgroup to the grid)."""
     b = q.shape[0]
     splits = num_splits or num_splits_for(b, k_cache.shape[1], block_tables.shape[1])
     if not 1 <= splits <= MAX_SPLITS:
