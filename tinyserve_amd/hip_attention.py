@@ -124,8 +124,8 @@ def num_splits_for(
 ) -> int:
     """Ranges to split each sequence's blocks into (triton_attention.py:499-510): enough
     for about ``target`` waves, at most ``MAX_SPLITS`` and the block-table width; 1 once
-    the batch alone gives ``no_split`` waves. Depends only on shapes, never on lengths,
-    so a captured graph always launches the same grid."""
+    the batch alone gives ``no_split`` waves. Its inputs are sizes only (no context
+    length is read), which keeps the grid of a graph-captured launch fixed."""
     target = TARGET_PROGRAMS if target is None else target
     no_split = NO_SPLIT_PROGRAMS if no_split is None else no_split
     programs = batch * num_kv_heads

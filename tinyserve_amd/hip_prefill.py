@@ -2,13 +2,18 @@
 reference's ``tinyserve.triton_prefill`` (src/tinyserve/triton_prefill.py:128-216), same
 arguments, result and errors, launching ``csrc/prefill.hip``.
 
-fp16 / bf16 with head_dim 64 or 128 run the MFMA kernel: a workgroup of four wave64s
-owns 32 queries x 4 query heads (or 64 x 2, 128 x 1) of one kv head, gathers each
-64-key tile of K and V from the paged cache into LDS once for all of them, computes
-S^T = K.Q^T and O^T += V^T.P^T with v_mfma_f32_32x32x16, and keeps an online softmax in
-fp32; P is rounded to the input dtype before P.V, as the reference kernel does
-(triton_prefill.py:118). fp32 inputs (exact fp32 dots, the reference's "ieee" path) and
-other head dims run the decode kernel's loop, one wave per (query row, kv head).
+fp16 / bf16 with head_dim 64 or 128 run the MFMA kernel (v_mfma_f32_32x32x16):
+S^T = K.Q^T and O^T += V^T.P^T with an online softmax in fp32, K and V tiles gathered
+from the paged cache into LDS by direct-to-LDS loads and shared by every wave of the
+workgroup. The library compiles three workgroup shapes and picks one from the launch's
+sizes: 8 waves over 64-key tiles (128 queries x 2 heads, a 3-stage ring; large launches),
+8 waves over 64 queries x 2 heads with the keys split into two halves walked by waves
+w and w + 4 and merged through LDS (launches too small to fill the chip), and 4 waves
+over 32-key tiles, three workgroups per CU (mid-size launches). fp16 P is rounded to
+fp16 before P.V, as the reference kernel rounds P to V's dtype (triton_prefill.py:118);
+bf16 P is carried as a hi + lo bf16 pair (two P.V MFMAs), since one bf16 rounding moves
+outputs past the tolerance. fp32 inputs (exact fp32 dots, the reference's "ieee" path)
+and other head dims run the decode kernel's loop, one wave per (query row, kv head).
 """
 
 from __future__ import annotations
