@@ -362,19 +362,16 @@ void paged_attend_kernel(const AttendArgs a) {
   // parked in LDS. The piece of split k walked by wave w takes slot k + w (+ cuts + W for
   // the second sequence of a length pair): along a sequence's blocks both k and w only
   // grow, and at least one of them grows from one piece to the next, so slots never
-  // collide. Slots no piece takes hold an empty state (m = -1e30, l = 0, acc = 0, which
-  // weighs 0), written before the walk; the merge takes every slot of a sequence in slot
-  // order (position order, so the result does not depend on timing).
+  // collide. Slots no piece takes are marked before the walk (m = -1e30) and skipped; the
+  // merge takes the other slots of a sequence in slot order (position order, so the
+  // result does not depend on timing).
   TokenState<T, D, HT, LB> st;
   extern __shared__ float lds_slots[];
   const StateSlots<HT, D> ss{lds_slots, CUT ? (pair ? 2 : 1) * (a.cuts + nw)
                                             : (pair ? 2 : 1) * (PREFILL ? 1 : a.wpg)};
   if constexpr (CUT) {
-    for (int i = threadIdx.x; i < ss.ns * HT; i += nw * kWave) {
-      lds_slots[i] = kNoMax;           // m
-      lds_slots[ss.ns * HT + i] = 0.f;  // l
-    }
-    for (int i = threadIdx.x; i < ss.ns * HT * D; i += nw * kWave) lds_slots[2 * ss.ns * HT + i] = 0.f;
+    // An unused slot is marked by its maximum alone; the merge skips it.
+    for (int i = threadIdx.x; i < ss.ns * HT; i += nw * kWave) lds_slots[i] = kNoMax;
     __syncthreads();
   }
   for (int sgi = 0; sgi < nseg; ++sgi) {
@@ -550,7 +547,9 @@ void paged_attend_kernel(const AttendArgs a) {
       for (int s2 = s0; s2 < s1; ++s2) mm = fmaxf(mm, ss.m(s2, g));
       float den = 0.f, num = 0.f;
       for (int s2 = s0; s2 < s1; ++s2) {
-        const float f = fast_exp2(ss.m(s2, g) - mm);
+        const float ms = ss.m(s2, g);
+        if (ms == kNoMax) continue;  // no piece (a piece has a token, so a finite maximum)
+        const float f = fast_exp2(ms - mm);
         den = fmaf(f, ss.l(s2, g), den);
         num = fmaf(f, ss.acc(s2, g, d), num);
       }
