@@ -513,3 +513,22 @@ def test_streaming_threshold() -> None:
         out = ha.launch_paged_decode_split(g.q, g.k_cache, g.v_cache, tables, g.context_lens, g.scale,
                                            g.block_size, num_splits=1)  # fmt: skip
         assert_matches(out, want, torch.bfloat16, f"width {width}")
+
+
+@pytest.mark.parametrize("splits", [4, 16])
+@pytest.mark.parametrize("lens", [[256] * 32, [1 + (389 * i) % 3000 for i in range(64)], [5000]])
+def test_in_workgroup_splits_replay_in_a_graph(splits: int, lens: list[int]) -> None:
+    # The in-group split launch (its LDS slot marking, barrier and merge) captured in a HIP
+    # graph: every replay, with unrelated eager work between replays, equals the eager
+    # launch bit for bit. One sequence of 5000 tokens takes the heavy register budget.
+    c = on_gpu(decode_case(lens, dtype=torch.float16, seed=len(lens) + splits))
+    want = ha.launch_paged_decode_split(*c.args(), c.scale, c.block_size, num_splits=splits)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        got = ha.launch_paged_decode_split(*c.args(), c.scale, c.block_size, num_splits=splits)
+    for _ in range(3):
+        got.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want)
+        torch.randn(1 << 20, device=DEVICE).sum().item()
