@@ -10,8 +10,8 @@
 // covers elements (i * LPT + c) * VEC .. + VEC - 1, so one load instruction of the LPT
 // lanes of a token reads LPT * 16 contiguous bytes. A wave therefore streams
 // TPW = 64 / LPT tokens per iteration (16 tokens of a 16-slot block for fp16 D=128:
-// 4 KB of K and 4 KB of V per wave per iteration, both issued before the previous
-// iteration's math so that three iterations are always in flight).
+// 4 KB of K and 4 KB of V per wave per iteration, issued before the previous
+// iteration's math so that two or three iterations are in flight, by register budget).
 //
 // Waves per workgroup. A decode launch gives each (sequence, head tile, split) a
 // workgroup of W = 1, 2, 4 (or, under the light budget below, 8) waves; wave w takes the
@@ -46,7 +46,7 @@ namespace ts {
 // Two register budgets. kHeavy: each lane streams 64 bytes of a head row per token, three
 // iterations in flight, one wave per SIMD (more than 256 VGPRs) -- for launches whose
 // waves all run in one round, where each wave must keep much in flight. kLight: 32 bytes
-// per lane, three in flight, two waves per SIMD -- for launches of several rounds, where
+// per lane, two in flight, two waves per SIMD -- for launches of several rounds, where
 // the second wave per SIMD hides each wave's start-up chain (lengths, block table, first
 // loads) and merge. (Tiles of four query heads stream 16 bytes per lane under it, or
 // their state would spill.) kLightStream is kLight with K/V read by non-temporal loads,
@@ -56,7 +56,10 @@ template <int B>
 struct BudgetOf {
   static constexpr bool kLightish = B != kHeavy;
   static constexpr int kLaneBytes = kLightish ? 32 : 64;
-  static constexpr int kNBuf = 3;
+  // Iterations in flight. Two under the light budgets: with two waves per SIMD a third
+  // only adds loads in flight past what HBM serves best (measured +0.3% to +2.5%
+  // with two, headline included).
+  static constexpr int kNBuf = kLightish ? 2 : 3;
   static constexpr int kWavesPerEU = kLightish ? 2 : 1;
 };
 
