@@ -143,33 +143,36 @@ struct TokenState {
   float acc[HT][S::kE];
 };
 
-// Merge the partial softmax states of lanes OFF apart (token lanes only: OFF >= LPT).
-template <int OFF, typename T, int D, int HT, int LB>
-__device__ __forceinline__ void merge_lanes(TokenState<T, D, HT, LB>& st) {
-  using S = RowShape<T, D, LB>;
-#pragma unroll
-  for (int g = 0; g < HT; ++g) {
-    const float mo = xor_lane<OFF>(st.m[g]);
-    const float lo = xor_lane<OFF>(st.l[g]);
-    const float mn = fmaxf(st.m[g], mo);
-    const float a1 = fast_exp2(st.m[g] - mn);
-    const float a2 = fast_exp2(mo - mn);
-    st.l[g] = st.l[g] * a1 + lo * a2;
-#pragma unroll
-    for (int e = 0; e < S::kE; ++e) st.acc[g][e] = st.acc[g][e] * a1 + xor_lane<OFF>(st.acc[g][e]) * a2;
-    st.m[g] = mn;
-  }
+template <int OFF, int L>
+__device__ __forceinline__ float token_lanes_max(float x) {
+  if constexpr (OFF < 64) return token_lanes_max<OFF * 2, L>(fmaxf(x, xor_lane<OFF>(x)));
+  return x;
+}
+template <int OFF>
+__device__ __forceinline__ float token_lanes_sum(float x) {
+  if constexpr (OFF < 64) return token_lanes_sum<OFF * 2>(x + xor_lane<OFF>(x));
+  return x;
 }
 
+// Merge the states of a wave's token lanes (lanes LPT, 2 LPT, ... apart) into one held
+// by every lane: the common maximum first, then each lane rescales its own state once
+// and the rescaled states are summed (one exponential per head instead of two per
+// exchange level).
 template <typename T, int D, int HT, int LB>
 __device__ __forceinline__ void merge_token_lanes(TokenState<T, D, HT, LB>& st) {
   constexpr int L = RowShape<T, D, LB>::kLPT;
-  if constexpr (L <= 1) merge_lanes<1>(st);
-  if constexpr (L <= 2) merge_lanes<2>(st);
-  if constexpr (L <= 4) merge_lanes<4>(st);
-  if constexpr (L <= 8) merge_lanes<8>(st);
-  if constexpr (L <= 16) merge_lanes<16>(st);
-  if constexpr (L <= 32) merge_lanes<32>(st);
+  using S = RowShape<T, D, LB>;
+  if constexpr (L < 64) {
+#pragma unroll
+    for (int g = 0; g < HT; ++g) {
+      const float mn = token_lanes_max<L, L>(st.m[g]);
+      const float f = fast_exp2(st.m[g] - mn);
+      st.l[g] = token_lanes_sum<L>(st.l[g] * f);
+#pragma unroll
+      for (int e = 0; e < S::kE; ++e) st.acc[g][e] = token_lanes_sum<L>(st.acc[g][e] * f);
+      st.m[g] = mn;
+    }
+  }
 }
 
 constexpr int kMaxWavesPerGroup = 4;  // heavy budget, and length pairs
