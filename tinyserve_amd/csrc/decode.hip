@@ -148,17 +148,34 @@ __device__ __forceinline__ float token_lanes_max(float x) {
   if constexpr (OFF < 64) return token_lanes_max<OFF * 2, L>(fmaxf(x, xor_lane<OFF>(x)));
   return x;
 }
-template <int OFF>
+// Sum over lanes OFF, 2 OFF, ... apart. DPP: the exchange folds into the add (row
+// rotations within 16 lanes, then v_permlane16_swap / v_permlane32_swap), the shorter
+// dependency chain for launches bound by latency; otherwise ds_swizzle / ds_bpermute,
+// which run beside the VALU for launches bound by issue.
+template <int OFF, bool DPP>
 __device__ __forceinline__ float token_lanes_sum(float x) {
-  if constexpr (OFF < 64) return token_lanes_sum<OFF * 2>(x + xor_lane<OFF>(x));
-  return x;
+  if constexpr (OFF >= 64) {
+    return x;
+  } else if constexpr (!DPP) {
+    return token_lanes_sum<OFF * 2, DPP>(x + xor_lane<OFF>(x));
+  } else if constexpr (OFF < 16) {
+    // Rotating each 16-lane row by OFF, 2 OFF, ..., 8 and adding sums the lanes of the
+    // row that agree mod OFF.
+    const float y = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + OFF, 0xf, 0xf, false));
+    return token_lanes_sum<OFF * 2, DPP>(x + y);
+  } else if constexpr (OFF == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return token_lanes_sum<32, DPP>(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+  } else {
+    return halves_sum(x);
+  }
 }
 
 // Merge the states of a wave's token lanes (lanes LPT, 2 LPT, ... apart) into one held
 // by every lane: the common maximum first, then each lane rescales its own state once
 // and the rescaled states are summed (one exponential per head instead of two per
 // exchange level).
-template <typename T, int D, int HT, int LB>
+template <bool DPP, typename T, int D, int HT, int LB>
 __device__ __forceinline__ void merge_token_lanes(TokenState<T, D, HT, LB>& st) {
   constexpr int L = RowShape<T, D, LB>::kLPT;
   using S = RowShape<T, D, LB>;
@@ -167,9 +184,9 @@ __device__ __forceinline__ void merge_token_lanes(TokenState<T, D, HT, LB>& st) 
     for (int g = 0; g < HT; ++g) {
       const float mn = token_lanes_max<L, L>(st.m[g]);
       const float f = fast_exp2(st.m[g] - mn);
-      st.l[g] = token_lanes_sum<L>(st.l[g] * f);
+      st.l[g] = token_lanes_sum<L, DPP>(st.l[g] * f);
 #pragma unroll
-      for (int e = 0; e < S::kE; ++e) st.acc[g][e] = token_lanes_sum<L>(st.acc[g][e] * f);
+      for (int e = 0; e < S::kE; ++e) st.acc[g][e] = token_lanes_sum<L, DPP>(st.acc[g][e] * f);
       st.m[g] = mn;
     }
   }
@@ -263,6 +280,8 @@ void paged_attend_kernel(const AttendArgs a) {
   constexpr int LB = BudgetOf<BUDGET>::kLightish && HT == 4 ? 16 : BudgetOf<BUDGET>::kLaneBytes;
   using S = RowShape<T, D, LB>;
   constexpr int LPT = S::kLPT, NV = S::kNV, VEC = S::kVec, TPW = S::kTPW, E = S::kE;
+  // Streaming launches are bound by issue, cached ones (short walks) by latency.
+  constexpr bool kDppMerge = BUDGET != kLightStream;
   constexpr int NBUF = BudgetOf<BUDGET>::kNBuf;
   const int lane = threadIdx.x % kWave;
   const int wave = PREFILL ? 0 : threadIdx.x / kWave;
@@ -514,7 +533,7 @@ void paged_attend_kernel(const AttendArgs a) {
           // A split boundary (a whole number of iterations past t0: the host runs cut
           // mode only when TPW divides the block size): park this piece, start the next.
           if (p0 + TPW == next_cut && next_cut < t1) {
-            merge_token_lanes(st);
+            merge_token_lanes<kDppMerge>(st);
             park_state(ss, st, slot++, tl == 0 ? c : -1);
 #pragma unroll
             for (int g = 0; g < HT; ++g) {
@@ -530,7 +549,7 @@ void paged_attend_kernel(const AttendArgs a) {
     }
   }
 
-  merge_token_lanes(st);
+  merge_token_lanes<kDppMerge>(st);
   if constexpr (CUT) {
     if (first < last) {
       park_state(ss, st, slot, tl == 0 ? c : -1);
