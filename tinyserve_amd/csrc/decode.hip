@@ -234,15 +234,88 @@ __device__ __forceinline__ void park_state(const Slots& ss, const State& st, int
   }
 }
 
-// The W waves of a decode workgroup each hold a merged state. They park it in LDS, then
+// Sum over lanes OFF, 2 OFF, ..., 8 apart (within each 16-lane row).
+template <int OFF, bool DPP>
+__device__ __forceinline__ float row_lanes_sum(float x) {
+  if constexpr (OFF >= 16) {
+    return x;
+  } else if constexpr (DPP) {
+    const float y = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + OFF, 0xf, 0xf, false));
+    return row_lanes_sum<OFF * 2, DPP>(x + y);
+  } else {
+    return row_lanes_sum<OFF * 2, DPP>(x + xor_lane<OFF>(x));
+  }
+}
+
+// Merge the token lanes' states and park the result in slot s. Common maximum and one
+// rescale per lane as in merge_token_lanes, then a reduce-scatter of the accumulators
+// over the token lanes 32 and 16 apart: v_permlane32_swap (v_permlane16_swap) of the
+// register pair (upper half, lower half) of the elements hands each lane its partner's
+// copy of the half it keeps (lanes 0-31, even rows: the upper half), so each level is
+// one swap and one add per pair, and halves what a lane holds. Token lanes closer than
+// 16 are summed whole. Each lane then writes its E / 4 (E / 2) elements.
+template <bool DPP, typename T, int D, int HT, int LB>
+__device__ __forceinline__ void merge_park(const StateSlots<HT, D>& ss, TokenState<T, D, HT, LB>& st,
+                                           int s) {
+  using S = RowShape<T, D, LB>;
+  constexpr int L = S::kLPT, E = S::kE, VEC = S::kVec;
+  const int lane = threadIdx.x % kWave;
+  if constexpr (L >= 64) {
+    park_state(ss, st, s, lane);
+  } else {
+    constexpr bool H32 = L <= 32, H16 = L <= 16;
+    constexpr int Q = E >> ((H32 ? 1 : 0) + (H16 ? 1 : 0));
+    int o = 0;
+    if constexpr (H32) o += lane < 32 ? E / 2 : 0;
+    if constexpr (H16) o += ((lane >> 4) & 1) == 0 ? E / 4 : 0;
+    const int c = lane % L;
+    const bool writer = L >= 16 || (lane & 15) < L;
+#pragma unroll
+    for (int g = 0; g < HT; ++g) {
+      const float mn = token_lanes_max<L, L>(st.m[g]);
+      const float f = fast_exp2(st.m[g] - mn);
+      const float l = token_lanes_sum<L, DPP>(st.l[g] * f);
+      float x[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) x[e] = st.acc[g][e] * f;
+      if constexpr (H32) {
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) {
+          const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x[E / 2 + i]), __float_as_uint(x[i]), false, false);
+          x[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+      }
+      if constexpr (H16) {
+#pragma unroll
+        for (int i = 0; i < E / 4; ++i) {
+          const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x[E / 4 + i]), __float_as_uint(x[i]), false, false);
+          x[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < Q; ++q) x[q] = row_lanes_sum<L, DPP>(x[q]);
+      if (lane == 0) {
+        ss.m(s, g) = mn;
+        ss.l(s, g) = l;
+      }
+      if (writer) {
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+          const int e = o + q;
+          ss.acc(s, g, ((e / VEC) * L + c) * VEC + e % VEC) = x[q];
+        }
+      }
+    }
+  }
+}
+
+// The W waves of a decode workgroup have each parked a merged state in slot w; then
 // thread t of the group produces output element t (of HT * D) by the two-partial rule
 // over the W states, and writes it either as the final output (one split) or as the
 // split's fp32 partial for the combine pass.
-template <typename T, int D, int HT, typename State, typename Args>
+template <typename T, int D, int HT, typename Args>
 __device__ __forceinline__ void merge_group_waves(const Args& a, const StateSlots<HT, D>& ss,
-                                                  const State& st, int wave, int c, int seq,
-                                                  int h0, int split, int64_t orow) {
-  park_state(ss, st, wave, c);
+                                                  int seq, int h0, int split, int64_t orow) {
   __syncthreads();
   const int W = a.wpg;
   for (int t = threadIdx.x; t < HT * D; t += W * kWave) {
@@ -533,8 +606,7 @@ void paged_attend_kernel(const AttendArgs a) {
           // A split boundary (a whole number of iterations past t0: the host runs cut
           // mode only when TPW divides the block size): park this piece, start the next.
           if (p0 + TPW == next_cut && next_cut < t1) {
-            merge_token_lanes<kDppMerge>(st);
-            park_state(ss, st, slot++, tl == 0 ? c : -1);
+            merge_park<kDppMerge>(ss, st, slot++);
 #pragma unroll
             for (int g = 0; g < HT; ++g) {
               st.m[g] = kNoMax;
@@ -549,13 +621,15 @@ void paged_attend_kernel(const AttendArgs a) {
     }
   }
 
-  merge_token_lanes<kDppMerge>(st);
+  // Parked states are merged across waves below; a one-wave workgroup writes its own.
   if constexpr (CUT) {
-    if (first < last) {
-      park_state(ss, st, slot, tl == 0 ? c : -1);
-    }
+    if (first < last) merge_park<kDppMerge>(ss, st, slot);
+  } else if (pair) {
+    merge_park<kDppMerge>(ss, st, 2 * wave + sgi);
+  } else if (!PREFILL && a.wpg > 1) {
+    merge_park<kDppMerge>(ss, st, wave);
   } else {
-    if (pair) park_state(ss, st, 2 * wave + sgi, tl == 0 ? c : -1);
+    merge_token_lanes<kDppMerge>(st);
   }
   }  // segments
   if constexpr (CUT) {
@@ -611,7 +685,7 @@ void paged_attend_kernel(const AttendArgs a) {
       return;
     }
     if (a.wpg > 1) {
-      merge_group_waves<T, D, HT>(a, ss, st, wave, tl == 0 ? c : -1, seq, h0, split, orow);
+      merge_group_waves<T, D, HT>(a, ss, seq, h0, split, orow);
       return;
     }
   }
