@@ -568,25 +568,26 @@ void paged_attend_kernel(const AttendArgs a) {
       for (int i = 0; i < NV; ++i)
 #pragma unroll
         for (int j = 0; j < VEC; ++j) vf32[i * VEC + j] = to_f32(vf[i].v[j]);
+      // The branch only rescales, in place; the update is common to both paths, so the
+      // state keeps its registers (two paths that each wrote a new state made the
+      // compiler copy it at their join).
       if (__any(grow)) {
 #pragma unroll
         for (int g = 0; g < HT; ++g) {
           const float mn = fmaxf(st.m[g], s[g]);
           const float al = fast_exp2(st.m[g] - mn);
-          const float p = fast_exp2(s[g] - mn);
-          st.l[g] = st.l[g] * al + p;
+          st.l[g] *= al;
 #pragma unroll
-          for (int e = 0; e < E; ++e) st.acc[g][e] = fmaf(p, vf32[e], st.acc[g][e] * al);
+          for (int e = 0; e < E; ++e) st.acc[g][e] *= al;
           st.m[g] = mn;
         }
-      } else {
+      }
 #pragma unroll
-        for (int g = 0; g < HT; ++g) {
-          const float p = fast_exp2(s[g] - st.m[g]);
-          st.l[g] += p;
+      for (int g = 0; g < HT; ++g) {
+        const float p = fast_exp2(s[g] - st.m[g]);
+        st.l[g] += p;
 #pragma unroll
-          for (int e = 0; e < E; ++e) st.acc[g][e] = fmaf(p, vf32[e], st.acc[g][e]);
-        }
+        for (int e = 0; e < E; ++e) st.acc[g][e] = fmaf(p, vf32[e], st.acc[g][e]);
       }
     };
 
@@ -607,13 +608,13 @@ void paged_attend_kernel(const AttendArgs a) {
           // mode only when TPW divides the block size): park this piece, start the next.
           if (p0 + TPW == next_cut && next_cut < t1) {
             merge_park<kDppMerge>(ss, st, slot++);
+            // Only the maximum is reset: a lane's first token of the next piece raises
+            // it and rescales the old l and acc by 2^(kNoMax - m) = 0, and a lane that
+            // sees no token of the piece keeps m = kNoMax, which the merge weighs by 0
+            // (every piece has a token, so the merged maximum is finite). Zeroing l and
+            // acc here made the compiler copy the whole state through every iteration.
 #pragma unroll
-            for (int g = 0; g < HT; ++g) {
-              st.m[g] = kNoMax;
-              st.l[g] = 0.f;
-#pragma unroll
-              for (int e = 0; e < E; ++e) st.acc[g][e] = 0.f;
-            }
+            for (int g = 0; g < HT; ++g) st.m[g] = kNoMax;
             next_cut += pc_tokens;
           }
         }
