@@ -528,7 +528,9 @@ void paged_attend_kernel(const AttendArgs a) {
     // NBUF iterations in flight: the loads of iteration i + NBUF - 1 are issued before
     // iteration i's math (ring of NBUF register buffers, indices fixed by unrolling).
     Pack16<T> kb[NBUF][NV], vb[NBUF][NV];
-    auto issue = [&](Pack16<T>(&kf)[NV], Pack16<T>(&vf)[NV], int p0) {
+    // A wave's own query row, already read: the target of issues past the range.
+    const T* const qdummy = qp + h0 * a.q_sh + c * VEC;
+    auto issue = [&](Pack16<T>(&kf)[NV], Pack16<T>(&vf)[NV], int p0, bool live) {
       if (((p0 >> lbs) - chunk) >= 64) {
         chunk += 64;
         win = (chunk + lane < last) ? btrow[chunk + lane] : 0;
@@ -539,14 +541,16 @@ void paged_attend_kernel(const AttendArgs a) {
       const int pe = pos < t1 ? pos : p0;
       const int blk = __shfl(win, (pe >> lbs) - chunk);
       const int64_t off = ((static_cast<int64_t>(blk) << lbs) + (pe & bs_mask)) * a.k_ss;
+      const T* const kp = live ? kbase + off : qdummy;
+      const T* const vp = live ? vbase + off : qdummy;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         if constexpr (BUDGET == kLightStream) {
-          kf[i].raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kbase + off + i * LPT * VEC));
-          vf[i].raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vbase + off + i * LPT * VEC));
+          kf[i].raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + i * LPT * VEC));
+          vf[i].raw = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vp + i * LPT * VEC));
         } else {
-          kf[i] = load16(kbase + off + i * LPT * VEC);
-          vf[i] = load16(vbase + off + i * LPT * VEC);
+          kf[i] = load16(kp + i * LPT * VEC);
+          vf[i] = load16(vp + i * LPT * VEC);
         }
       }
     };
@@ -592,8 +596,12 @@ void paged_attend_kernel(const AttendArgs a) {
     };
 
 #pragma unroll
+    // Every issue is unconditional: one past the range reads the wave's query row
+    // instead (cached; its table lookup uses a position in range). A conditional issue
+    // makes the compiler's load counting allow for the path where nothing was issued, and
+    // each iteration's wait for its own data then also waits for the loads just issued.
     for (int j = 0; j + 1 < NBUF; ++j)
-      if (t0 + j * TPW < t1) issue(kb[j], vb[j], t0 + j * TPW);
+      issue(kb[j], vb[j], t0 + j * TPW < t1 ? t0 + j * TPW : t0, t0 + j * TPW < t1);
     if constexpr (CUT) cut_setup();
     for (int base = t0; base < t1; base += NBUF * TPW) {
 #pragma unroll
@@ -601,7 +609,7 @@ void paged_attend_kernel(const AttendArgs a) {
         const int p0 = base + j * TPW;
         if (p0 >= t1) break;
         const int pn = p0 + (NBUF - 1) * TPW;
-        if (pn < t1) issue(kb[(j + NBUF - 1) % NBUF], vb[(j + NBUF - 1) % NBUF], pn);
+        issue(kb[(j + NBUF - 1) % NBUF], vb[(j + NBUF - 1) % NBUF], pn < t1 ? pn : p0, pn < t1);
         attend(kb[j], vb[j], p0);
         if constexpr (CUT) {
           // A split boundary (a whole number of iterations past t0: the host runs cut
