@@ -249,10 +249,12 @@ def test_baseline_config_2() -> None:
     ([700, 31, 1200], (16, 8), torch.float16, 32),
 ])  # fmt: skip
 @pytest.mark.parametrize("splits", [2, 3, 4, 7, 16])
-def test_in_workgroup_splits_match_the_hbm_partials(case: tuple, splits: int) -> None:
+def test_in_workgroup_splits_match_the_hbm_partials(case: tuple, splits: int, monkeypatch) -> None:
     # An explicit split count merges the ranges' states in LDS (one launch); the same
     # ranges as HBM partials + the combine launch must give the same output up to fp32
-    # summation order, and both the oracle's.
+    # summation order, and both the oracle's. The small grids here would take the HBM
+    # form under the launcher's policy: the in-group path is forced for every case.
+    monkeypatch.setattr(ha, "IN_GROUP_MIN_WAVES", 0)
     lens, (hq, hkv), dtype, bs = case
     c = decode_case(lens, hq, hkv, dtype=dtype, block_size=bs, seed=len(lens) + splits)
     g = on_gpu(c)
@@ -517,10 +519,12 @@ def test_streaming_threshold() -> None:
 
 @pytest.mark.parametrize("splits", [4, 16])
 @pytest.mark.parametrize("lens", [[256] * 32, [1 + (389 * i) % 3000 for i in range(64)], [5000]])
-def test_in_workgroup_splits_replay_in_a_graph(splits: int, lens: list[int]) -> None:
+def test_in_workgroup_splits_replay_in_a_graph(splits: int, lens: list[int], monkeypatch) -> None:
     # The in-group split launch (its LDS slot marking, barrier and merge) captured in a HIP
     # graph: every replay, with unrelated eager work between replays, equals the eager
-    # launch bit for bit. One sequence of 5000 tokens takes the heavy register budget.
+    # launch bit for bit. One sequence of 5000 tokens takes the heavy register budget
+    # (forced in-group: the launcher's policy gives so small a grid the HBM form).
+    monkeypatch.setattr(ha, "IN_GROUP_MIN_WAVES", 0)
     c = on_gpu(decode_case(lens, dtype=torch.float16, seed=len(lens) + splits))
     want = ha.launch_paged_decode_split(*c.args(), c.scale, c.block_size, num_splits=splits)
     g = torch.cuda.CUDAGraph()
@@ -532,3 +536,21 @@ def test_in_workgroup_splits_replay_in_a_graph(splits: int, lens: list[int]) -> 
         torch.cuda.synchronize()
         assert torch.equal(got, want)
         torch.randn(1 << 20, device=DEVICE).sum().item()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lens,splits", [([8192] * 4, None), ([32768], None), ([4096] * 8, 8)])
+def test_small_grids_take_the_hbm_partials(lens: list[int], splits: int | None) -> None:
+    # A split count on a grid too small to fill the chip runs S workgroups per (sequence,
+    # head tile) writing fp32 partials, then the combine: same output as the in-group form
+    # up to fp32 summation order, and the oracle's.
+    c = decode_case(lens, 16, 8, dtype=torch.float16, seed=len(lens))
+    g = on_gpu(c)
+    plan = ha.decode_plan(len(lens), 16, 8, 128, c.block_size, g.block_tables.shape[1], 1)
+    gx, gy, gz = plan["grid"]
+    assert gx * gy * gz * plan["waves_per_group"] < ha.IN_GROUP_MIN_WAVES
+    out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, num_splits=splits)
+    s = splits or ha._policy_splits(g.q, g.k_cache, g.block_tables, c.block_size)
+    assert s > 1
+    torch.testing.assert_close(out.float(), hbm_split_combine(g, s).float(), atol=0, rtol=0)
+    assert_matches(out, oracle32(c), torch.float16, f"{lens} splits={splits}")

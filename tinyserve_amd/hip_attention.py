@@ -23,6 +23,7 @@ reference's does (:361-391).
 from __future__ import annotations
 
 import ctypes
+import functools
 
 import torch
 
@@ -57,6 +58,11 @@ MAX_SPLITS = 16
 # tokens: 10.0 us against 21.5 us for 4 partials + combine). More splits, and any count
 # a caller asks for, write partials and combine them.
 IN_GROUP_SPLITS = 4
+# A split count S > 1 runs inside the one-split grid's workgroups (the ranges' states
+# merged in LDS, one launch) only when that grid has at least this many waves, one per
+# SIMD of the chip; a smaller grid leaves most of the chip idle, and S workgroups per
+# (sequence, head tile) writing fp32 partials, then the combine, finish sooner.
+IN_GROUP_MIN_WAVES = 1024
 
 # Reference constants, kept for ``num_splits_for(..., target=..., no_split=...)`` callers
 # that want the T4 policy exactly.
@@ -152,6 +158,34 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
             "head_tile": out[3], "grid": (out[4], out[5], out[6]), "lds_bytes": out[7]}  # fmt: skip
 
 
+@functools.lru_cache(maxsize=512)
+def _one_split_waves(device: int, b: int, hq: int, hkv: int, d: int, block_size: int, width: int,
+                     dtype: torch.dtype) -> int:  # fmt: skip
+    """Waves of the one-split launch of these sizes on ``device`` (which sets the CU count)."""
+    p = decode_plan(b, hq, hkv, d, block_size, width, 1, 0, dtype)
+    gx, gy, gz = p["grid"]
+    return gx * gy * gz * int(p["waves_per_group"])
+
+
+def _policy_splits(q: torch.Tensor, k_cache: torch.Tensor, block_tables: torch.Tensor,
+                   block_size: int) -> int:  # fmt: skip
+    """The split count when the caller gives none. A one-split grid of at least half
+    ``IN_GROUP_MIN_WAVES`` waves keeps ``num_splits_for``'s count, and a count up to
+    ``IN_GROUP_SPLITS`` becomes one launch whose workgroups split each sequence over their
+    waves. A smaller grid gets enough split ranges for about 2 x ``IN_GROUP_MIN_WAVES``
+    waves (at most ``MAX_SPLITS`` and the table width), as fp32 partials and the combine.
+    Sizes only: a graph-captured launch keeps its grid."""
+    b, hq, d = q.shape
+    if b == 0 or not q.is_cuda:  # nothing to launch, or the launch raises
+        return 1
+    hkv, width = k_cache.shape[1], block_tables.shape[1]
+    splits = num_splits_for(b, hkv, width)
+    waves = _one_split_waves(q.device.index, b, hq, hkv, d, block_size, width, q.dtype)
+    if waves >= IN_GROUP_MIN_WAVES // 2:
+        return 1 if splits <= IN_GROUP_SPLITS else splits
+    return max(splits, min(-(-2 * IN_GROUP_MIN_WAVES // max(waves, 1)), MAX_SPLITS, width))
+
+
 def _launch(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -182,17 +216,19 @@ def _launch(
                   scale, dt, stream)  # fmt: skip
         return out
     # The split ranges inside each workgroup: every range's softmax state is merged with
-    # the others in LDS, and the result written once. Shapes it cannot take (blocks
-    # smaller than a loop iteration's tokens, or more states than its LDS holds) write
-    # fp32 partials to HBM and combine them in a second launch.
-    rc = _lib.call_status("ts_decode_split", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                          block_tables.data_ptr(), context_lens.data_ptr(), out.data_ptr(),
-                          None, None, None, b, hq, hkv, d, block_size, *strides, width, splits,
-                          head_tile, scale, dt, stream)  # fmt: skip
-    if rc == 0:
-        return out
-    if rc != _lib.TS_EUNSUPPORTED:
-        raise ValueError(f"ts_decode_split: {_lib.load().ts_strerror(rc).decode()}")
+    # the others in LDS, and the result written once. Grids too small to fill the chip,
+    # and shapes the kernel cannot cut (blocks smaller than a loop iteration's tokens, or
+    # more states than its LDS holds), write fp32 partials to HBM and combine them in a
+    # second launch.
+    if _one_split_waves(dev, b, hq, hkv, d, block_size, width, q.dtype) >= IN_GROUP_MIN_WAVES:
+        rc = _lib.call_status("ts_decode_split", q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                              block_tables.data_ptr(), context_lens.data_ptr(), out.data_ptr(),
+                              None, None, None, b, hq, hkv, d, block_size, *strides, width, splits,
+                              head_tile, scale, dt, stream)  # fmt: skip
+        if rc == 0:
+            return out
+        if rc != _lib.TS_EUNSUPPORTED:
+            raise ValueError(f"ts_decode_split: {_lib.load().ts_strerror(rc).decode()}")
     m = torch.empty((b, hq, splits), dtype=torch.float32, device=q.device)
     l = torch.empty_like(m)  # noqa: E741
     acc = torch.empty((b, hq, splits, d), dtype=torch.float32, device=q.device)
@@ -317,19 +353,19 @@ def launch_paged_decode_split(
 
     An explicit ``num_splits`` S > 1 computes what the reference computes: S block
     ranges of ``ceil(blocks / S)``, each with its own softmax state (m, l, acc), merged
-    by the two-partial rule. The states stay in each workgroup's LDS and the merge runs
-    in the same launch (fp32 partials in HBM and a second launch only for shapes that
-    cannot: block sizes under a loop iteration's tokens). Without a count, it comes
-    from ``num_splits_for(B, Hkv, max_blocks)``, and a policy count up to
+    by the two-partial rule. When the one-split grid fills the chip (``IN_GROUP_MIN_WAVES``)
+    the states stay in each workgroup's LDS and the merge runs in the same launch;
+    smaller grids, and block sizes under a loop iteration's tokens, write fp32 partials
+    to HBM and combine them in a second launch. Without a count, it comes
+    from ``_policy_splits``: ``num_splits_for(B, Hkv, max_blocks)``, where a count up to
     ``IN_GROUP_SPLITS`` becomes one launch whose workgroups split each sequence over
-    their waves (the library sizes the workgroup to the grid)."""
-    b = q.shape[0]
-    splits = num_splits or num_splits_for(b, k_cache.shape[1], block_tables.shape[1])
-    if not 1 <= splits <= MAX_SPLITS:
-        raise ValueError(f"num_splits must be 1..{MAX_SPLITS}, got {splits}")
+    their waves (the library sizes the workgroup to the grid), raised for grids too
+    small to fill the chip."""
+    if num_splits and not 1 <= num_splits <= MAX_SPLITS:
+        raise ValueError(f"num_splits must be 1..{MAX_SPLITS}, got {num_splits}")
     check_tile(tile or DECODE_TILE)
-    if not num_splits and splits <= IN_GROUP_SPLITS:  # no count given (None or 0): the policy
-        splits = 1
+    # No count given (None or 0): the policy.
+    splits = num_splits or _policy_splits(q, k_cache, block_tables, block_size)
     return _launch(q, k_cache, v_cache, block_tables, context_lens, scale, block_size, splits, 0)
 
 
@@ -351,11 +387,9 @@ def launch_paged_decode_split_noalloc(
     ``launch_paged_decode_split``; a launch whose partials exceed the scratch raises
     ValueError before anything runs. Calls that overlap in time on one device race."""
     b, hq, d = q.shape
-    splits = num_splits or num_splits_for(b, k_cache.shape[1], block_tables.shape[1])
-    if not 1 <= splits <= MAX_SPLITS:
-        raise ValueError(f"num_splits must be 1..{MAX_SPLITS}, got {splits}")
-    if not num_splits and splits <= IN_GROUP_SPLITS:  # no count given (None or 0): the policy
-        splits = 1
+    if num_splits and not 1 <= num_splits <= MAX_SPLITS:
+        raise ValueError(f"num_splits must be 1..{MAX_SPLITS}, got {num_splits}")
+    splits = num_splits or _policy_splits(q, k_cache, block_tables, block_size)
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
         raise ValueError(f"out must be like q {tuple(q.shape)} {q.dtype}")
     dev = _lib.require_device(q, k_cache, v_cache, block_tables, context_lens, out)
