@@ -554,3 +554,29 @@ def test_small_grids_take_the_hbm_partials(lens: list[int], splits: int | None) 
     assert s > 1
     torch.testing.assert_close(out.float(), hbm_split_combine(g, s).float(), atol=0, rtol=0)
     assert_matches(out, oracle32(c), torch.float16, f"{lens} splits={splits}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lens", [[32768], [8192] * 4, [4096] * 8])
+def test_small_grid_policy_replays_in_a_graph(lens: list[int]) -> None:
+    # The policy's HBM-partials launch for a small grid (partials allocated inside the
+    # capture, from the graph's pool, then the combine) captured in a HIP graph: every
+    # replay, with eager work between replays, equals the eager launch bit for bit, and
+    # neither form synchronizes with the host.
+    c = on_gpu(decode_case(lens, dtype=torch.float16, seed=len(lens)))
+    want = ha.launch_paged_decode_split(*c.args(), c.scale, c.block_size)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        ha.launch_paged_decode_split(*c.args(), c.scale, c.block_size)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            got = ha.launch_paged_decode_split(*c.args(), c.scale, c.block_size)
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    for _ in range(3):
+        got.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(got, want, atol=0, rtol=0)
+        torch.randn(1 << 20, device=DEVICE).sum()  # unrelated eager work between replays
