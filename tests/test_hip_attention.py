@@ -478,7 +478,7 @@ def test_combine_over_many_splits(splits: int, head_dim: int, dtype: torch.dtype
 def test_streaming_launches(dtype: torch.dtype, head_dim: int, heads: tuple[int, int], head_tile: int) -> None:
     # A table wide enough to bound more than 256 MiB of K/V makes the launch stream K/V
     # with non-temporal loads (light budget, one round of workgroups; tiles of four query
-    # heads take the heavy budget's cached loads instead); the unused columns
+    # heads and 64-element rows take the heavy budget's cached loads instead); the unused columns
     # are never read. Head groups of 2, 4 and 1 (tiles of 2, 4 and 1 query heads) and the
     # per-head launch; 32 sequences give length pairs at one split. The results match the
     # oracle and the launch over the tight table, for one split and for HBM splits.
@@ -491,8 +491,10 @@ def test_streaming_launches(dtype: torch.dtype, head_dim: int, heads: tuple[int,
     wide[:, :w] = g.block_tables
     for splits in (1, 4):
         plan = ha.decode_plan(b, *heads, head_dim, g.block_size, 8192, splits, head_tile, dtype)
-        # Tiles of four query heads run the heavy budget with cached loads; the others stream.
-        assert plan["budget"] == ("heavy" if plan["head_tile"] == 4 else "light_stream"), plan
+        # Tiles of four query heads and rows of 64 elements run the heavy budget with cached
+        # loads; the others stream.
+        heavy = plan["head_tile"] == 4 or head_dim == 64
+        assert plan["budget"] == ("heavy" if heavy else "light_stream"), plan
         tight = ha._launch(*g.args(), g.scale, g.block_size, splits, head_tile)
         out = ha._launch(g.q, g.k_cache, g.v_cache, wide, g.context_lens, g.scale, g.block_size, splits,
                          head_tile)  # fmt: skip

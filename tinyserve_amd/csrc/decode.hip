@@ -1025,8 +1025,10 @@ static int plan_decode(int B, int Hq, int Hkv, int D, int block_size, int max_bl
   // of eight) read them from L2. Measured against the light streaming launch: 64 x 4096
   // with 32 / 8 heads 207 -> 193 us, 128 x 4096 407 -> 379 us, 64 / 8 heads 406 -> 328
   // us, 16 x 8192 bf16 208 -> 158 us; with non-temporal loads the heavy launch took
-  // 212, 424, 426 and 186 us.
-  const bool heavy_stream = stream_kv && ht == 4;
+  // 212, 424, 426 and 186 us. Rows of 64 elements likewise (64 x 4096 130 -> 120 us,
+  // 64 x 8192 257 -> 233 us); two-head tiles of 128-element rows keep the light budget
+  // (the heavy one: 184 against 160 us at 64 x 4096).
+  const bool heavy_stream = stream_kv && (ht == 4 || D == 64);
   if (stream_kv && by_length) wpg = heavy_stream ? kMaxWavesPerGroup : kMaxWavesLight;
   const bool light = (stream_kv && !heavy_stream) ||
                      (!stream_kv && light_budget(grid_waves, max_blocks > 0 && walk < 512));
