@@ -550,9 +550,8 @@ def test_small_grids_take_the_hbm_partials(lens: list[int], splits: int | None) 
     # up to fp32 summation order, and the oracle's.
     c = decode_case(lens, 16, 8, dtype=torch.float16, seed=len(lens))
     g = on_gpu(c)
-    plan = ha.decode_plan(len(lens), 16, 8, 128, c.block_size, g.block_tables.shape[1], 1)
-    gx, gy, gz = plan["grid"]
-    assert gx * gy * gz * plan["waves_per_group"] < ha.IN_GROUP_MIN_WAVES
+    simds = ha._one_split_waves(0, len(lens), 16, 8, 128, c.block_size, g.block_tables.shape[1], torch.float16)
+    assert simds < ha.IN_GROUP_MIN_WAVES
     out = ha.launch_paged_decode_split(*g.args(), c.scale, c.block_size, num_splits=splits)
     s = splits or ha._policy_splits(g.q, g.k_cache, g.block_tables, c.block_size)
     assert s > 1

@@ -59,9 +59,10 @@ MAX_SPLITS = 16
 # a caller asks for, write partials and combine them.
 IN_GROUP_SPLITS = 4
 # A split count S > 1 runs inside the one-split grid's workgroups (the ranges' states
-# merged in LDS, one launch) only when that grid has at least this many waves, one per
-# SIMD of the chip; a smaller grid leaves most of the chip idle, and S workgroups per
-# (sequence, head tile) writing fp32 partials, then the combine, finish sooner.
+# merged in LDS, one launch) only when that grid occupies at least this many SIMDs (one
+# wave per SIMD under the heavy budget, two under the light ones), the whole chip; a
+# smaller grid leaves most of the chip idle, and S workgroups per (sequence, head tile)
+# writing fp32 partials, then the combine, finish sooner.
 IN_GROUP_MIN_WAVES = 1024
 
 # Reference constants, kept for ``num_splits_for(..., target=..., no_split=...)`` callers
@@ -161,20 +162,22 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
 @functools.lru_cache(maxsize=512)
 def _one_split_waves(device: int, b: int, hq: int, hkv: int, d: int, block_size: int, width: int,
                      dtype: torch.dtype) -> int:  # fmt: skip
-    """Waves of the one-split launch of these sizes on ``device`` (which sets the CU count)."""
+    """SIMDs the one-split launch of these sizes occupies on ``device`` (which sets the CU
+    count): its waves, over the two waves per SIMD of the light budgets."""
     p = decode_plan(b, hq, hkv, d, block_size, width, 1, 0, dtype)
     gx, gy, gz = p["grid"]
-    return gx * gy * gz * int(p["waves_per_group"])
+    waves = gx * gy * gz * int(p["waves_per_group"])
+    return waves // 2 if p["budget"] in ("light", "light_stream") else waves
 
 
 def _policy_splits(q: torch.Tensor, k_cache: torch.Tensor, block_tables: torch.Tensor,
                    block_size: int) -> int:  # fmt: skip
-    """The split count when the caller gives none. A one-split grid of at least half
-    ``IN_GROUP_MIN_WAVES`` waves keeps ``num_splits_for``'s count, and a count up to
+    """The split count when the caller gives none. A one-split grid occupying at least half
+    ``IN_GROUP_MIN_WAVES`` SIMDs keeps ``num_splits_for``'s count, and a count up to
     ``IN_GROUP_SPLITS`` becomes one launch whose workgroups split each sequence over their
-    waves. A smaller grid gets enough split ranges for about 2 x ``IN_GROUP_MIN_WAVES``
-    waves (at most ``MAX_SPLITS`` and the table width), as fp32 partials and the combine.
-    Sizes only: a graph-captured launch keeps its grid."""
+    waves. A smaller grid gets enough split ranges for about twice the chip (at most
+    ``MAX_SPLITS`` and the table width), as fp32 partials and the combine. Sizes only: a
+    graph-captured launch keeps its grid."""
     b, hq, d = q.shape
     if b == 0 or not q.is_cuda:  # nothing to launch, or the launch raises
         return 1
