@@ -1030,10 +1030,12 @@ static int plan_decode(int B, int Hq, int Hkv, int D, int block_size, int max_bl
   // (the heavy one: 184 against 160 us at 64 x 4096).
   const bool heavy_stream = stream_kv && (ht == 4 || D == 64);
   if (stream_kv && by_length) wpg = heavy_stream ? kMaxWavesPerGroup : kMaxWavesLight;
-  // Cached launches of two-head tiles of 16-bit 128-element rows: the light budget at
-  // any walk length (measured against heavy: equal or faster on every shape from 32 x 256
-  // to 64 x 1024 and 24 x 2048, e.g. 64 x 1024 45.2 -> 42.1 us).
-  const bool light_rows = ht <= 2 && D == 128 && dtype != TS_F32;
+  // Cached launches of two-head tiles of 16-bit 128- or 64-element rows: the light budget
+  // at any walk length (measured against heavy: equal or faster on every shape from
+  // 32 x 256 to 64 x 1024 and 24 x 2048, e.g. 64 x 1024 45.2 -> 42.1 us; D=64 64 x 1024
+  // 26.4 -> 23.5 us, 128 x 1024 54.1 -> 44.4 us). Four-head tiles keep the rule below
+  // (64 x 1024 with 32 / 8 heads: heavy 49.1, light 77.7 us).
+  const bool light_rows = ht <= 2 && (D == 128 || D == 64) && dtype != TS_F32;
   const bool light = (stream_kv && !heavy_stream) ||
                      (!stream_kv && (light_rows || light_budget(grid_waves, max_blocks > 0 && walk < 512)));
   // With two waves per SIMD the chip holds twice the waves: up to 8 per workgroup, so
