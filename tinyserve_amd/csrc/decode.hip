@@ -143,9 +143,10 @@ struct TokenState {
   float acc[HT][S::kE];
 };
 
-template <int OFF, int L>
+// Max over lanes OFF, 2 OFF, ... apart.
+template <int OFF>
 __device__ __forceinline__ float token_lanes_max(float x) {
-  if constexpr (OFF < 64) return token_lanes_max<OFF * 2, L>(fmaxf(x, xor_lane<OFF>(x)));
+  if constexpr (OFF < 64) return token_lanes_max<OFF * 2>(fmaxf(x, xor_lane<OFF>(x)));
   return x;
 }
 // Sum over lanes OFF, 2 OFF, ... apart. DPP: the exchange folds into the add (row
@@ -182,7 +183,7 @@ __device__ __forceinline__ void merge_token_lanes(TokenState<T, D, HT, LB>& st) 
   if constexpr (L < 64) {
 #pragma unroll
     for (int g = 0; g < HT; ++g) {
-      const float mn = token_lanes_max<L, L>(st.m[g]);
+      const float mn = token_lanes_max<L>(st.m[g]);
       const float f = fast_exp2(st.m[g] - mn);
       st.l[g] = token_lanes_sum<L, DPP>(st.l[g] * f);
 #pragma unroll
@@ -272,7 +273,7 @@ __device__ __forceinline__ void merge_park(const StateSlots<HT, D>& ss, TokenSta
     const bool writer = L >= 16 || (lane & 15) < L;
 #pragma unroll
     for (int g = 0; g < HT; ++g) {
-      const float mn = token_lanes_max<L, L>(st.m[g]);
+      const float mn = token_lanes_max<L>(st.m[g]);
       const float f = fast_exp2(st.m[g] - mn);
       const float l = token_lanes_sum<L, DPP>(st.l[g] * f);
       float x[E];
