@@ -648,19 +648,45 @@ void paged_attend_kernel(const AttendArgs a) {
     // several pieces, merged by the same rule).
     __syncthreads();
     const int parts = pair && pair_b >= 0 ? 2 : 1;
+    const int nsl = a.cuts + nw;  // slots per sequence (at most 16 + 8)
     for (int t = threadIdx.x; t < parts * HT * D; t += nw * kWave) {
       const int pi = t / (HT * D);
       const int g = (t % (HT * D)) / D, d = t % D;
-      const int s0 = pi * (a.cuts + nw), s1 = s0 + a.cuts + nw;
-      float mm = kNoMax;
-      for (int s2 = s0; s2 < s1; ++s2) mm = fmaxf(mm, ss.m(s2, g));
+      const int s0 = pi * nsl;
       float den = 0.f, num = 0.f;
-      for (int s2 = s0; s2 < s1; ++s2) {
-        const float ms = ss.m(s2, g);
-        if (ms == kNoMax) continue;  // no piece (a piece has a token, so a finite maximum)
-        const float f = fast_exp2(ms - mm);
-        den = fmaf(f, ss.l(s2, g), den);
-        num = fmaf(f, ss.acc(s2, g, d), num);
+      if constexpr (D % kWave == 0) {
+        // A wave's 64 outputs share (sequence, head): lane s takes slot s's maximum and
+        // denominator, the wave forms every slot's weight at once (one exponential per
+        // lane), and the weights are broadcast slot by slot for the accumulators.
+        // An unused slot has only its maximum written: its other fields are never read.
+        const float ms = lane < nsl ? ss.m(s0 + lane, g) : kNoMax;
+        const float ls = ms != kNoMax ? ss.l(s0 + lane, g) : 0.f;
+        float mm = ms;
+        mm = fmaxf(mm, xor_lane<1>(mm));
+        mm = fmaxf(mm, xor_lane<2>(mm));
+        mm = fmaxf(mm, xor_lane<4>(mm));
+        mm = fmaxf(mm, xor_lane<8>(mm));
+        mm = fmaxf(mm, xor_lane<16>(mm));
+        mm = halves_max(mm);
+        // No piece: the slot's maximum is kNoMax, its weight 0 (a piece has a token, so
+        // a finite maximum).
+        const float f = ms == kNoMax ? 0.f : fast_exp2(ms - mm);
+        den = group_sum<64>(ms != kNoMax ? f * ls : 0.f);
+        for (int s2 = 0; s2 < nsl; ++s2) {
+          const float fs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), s2));
+          if (fs != 0.f) num = fmaf(fs, ss.acc(s0 + s2, g, d), num);
+        }
+      } else {
+        const int s1 = s0 + nsl;
+        float mm = kNoMax;
+        for (int s2 = s0; s2 < s1; ++s2) mm = fmaxf(mm, ss.m(s2, g));
+        for (int s2 = s0; s2 < s1; ++s2) {
+          const float ms = ss.m(s2, g);
+          if (ms == kNoMax) continue;  // no piece (a piece has a token, so a finite maximum)
+          const float f = fast_exp2(ms - mm);
+          den = fmaf(f, ss.l(s2, g), den);
+          num = fmaf(f, ss.acc(s2, g, d), num);
+        }
       }
       const int64_t row = static_cast<int64_t>(pi ? pair_b : (pair ? pair_a : seq)) * a.o_sb;
       static_cast<T*>(a.out)[row + (h0 + g) * a.o_sh + d] = from_f32<T>(num / den);
