@@ -127,6 +127,39 @@ def test_decode_launch_plans(lib: ctypes.CDLL) -> None:
         plan(8, 12, 8, 128, 16, 8, 1)
 
 
+def test_decode_budget_choices(lib: ctypes.CDLL) -> None:
+    # Which register budget a launch runs (sizes only). Streaming launches (K/V bounded by
+    # the table width above 256 MiB): light-stream for two-head tiles of 128-element rows,
+    # the heavy budget's cached loads for four-head tiles and 64-element rows. Cached
+    # launches of two-head 16-bit tiles: light at any walk length; fp32 and four-head
+    # tiles keep the walk rule (heavy for long walks on one round of waves).
+    plan = hip_attention.decode_plan
+    assert plan(64, 16, 8, 128, 16, 256, 1)["budget"] == "light_stream"
+    assert plan(64, 32, 8, 128, 16, 256, 1)["budget"] == "heavy"  # four-head tiles
+    assert plan(64, 32, 8, 128, 16, 256, 1)["head_tile"] == 4
+    assert plan(64, 16, 8, 64, 16, 512, 1)["budget"] == "heavy"  # D=64, 512 MiB bound
+    assert plan(64, 16, 8, 128, 16, 64, 1)["budget"] == "light"  # 64 x 1024, cached
+    assert plan(16, 16, 8, 128, 16, 128, 1, dtype=torch.bfloat16)["budget"] == "light"
+    assert plan(64, 16, 8, 64, 16, 64, 1)["budget"] == "light"  # D=64, cached
+    assert plan(64, 32, 8, 128, 16, 64, 1)["budget"] == "heavy"  # four heads, long walks
+    assert plan(8, 16, 8, 128, 16, 256, 1, dtype=torch.float32)["budget"] == "heavy"
+
+
+def test_policy_splits_for_small_grids(lib: ctypes.CDLL) -> None:
+    # The launcher's split count with none given (sizes only; 256 CUs assumed without a
+    # device): num_splits_for's count, one launch for counts up to 4 on grids of at least
+    # half the chip's SIMDs, and more ranges (at most 16 and the table width) for smaller
+    # grids.
+    def policy(b: int, width: int) -> int:
+        return hip_attention.policy_splits(b, 16, 8, 128, 16, width)
+
+    assert policy(64, 256) == 1  # the metric: one launch
+    assert policy(32, 16) == 1  # config 2 without a count
+    assert policy(1, 2048) == 16  # one long sequence: 16 ranges of partials
+    assert policy(8, 256) == 8
+    assert policy(16, 128) == 1  # half the chip: one launch
+
+
 # --- decode entry points: the reference's argument errors (test_triton_attention.py:201-234)
 
 

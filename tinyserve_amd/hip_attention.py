@@ -170,23 +170,32 @@ def _one_split_waves(device: int, b: int, hq: int, hkv: int, d: int, block_size:
     return waves // 2 if p["budget"] in ("light", "light_stream") else waves
 
 
+def policy_splits(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
+                  max_blocks: int, dtype: torch.dtype = torch.float16, device: int = -1) -> int:  # fmt: skip
+    """The split count the launcher uses when the caller gives none. A one-split grid
+    occupying at least half ``IN_GROUP_MIN_WAVES`` SIMDs keeps ``num_splits_for``'s count,
+    and a count up to ``IN_GROUP_SPLITS`` becomes one launch whose workgroups split each
+    sequence over their waves. A smaller grid gets enough split ranges for about twice
+    the chip (at most ``MAX_SPLITS`` and the table width), as fp32 partials and the
+    combine. Sizes only (``device`` sets the CU count): a graph-captured launch keeps its
+    grid."""
+    splits = num_splits_for(batch, num_kv_heads, max_blocks)
+    simds = _one_split_waves(device, batch, num_q_heads, num_kv_heads, head_dim, block_size,
+                             max_blocks, dtype)  # fmt: skip
+    if simds >= IN_GROUP_MIN_WAVES // 2:
+        return 1 if splits <= IN_GROUP_SPLITS else splits
+    return max(splits, min(-(-2 * IN_GROUP_MIN_WAVES // max(simds, 1)), MAX_SPLITS, max_blocks))
+
+
 def _policy_splits(q: torch.Tensor, k_cache: torch.Tensor, block_tables: torch.Tensor,
                    block_size: int) -> int:  # fmt: skip
-    """The split count when the caller gives none. A one-split grid occupying at least half
-    ``IN_GROUP_MIN_WAVES`` SIMDs keeps ``num_splits_for``'s count, and a count up to
-    ``IN_GROUP_SPLITS`` becomes one launch whose workgroups split each sequence over their
-    waves. A smaller grid gets enough split ranges for about twice the chip (at most
-    ``MAX_SPLITS`` and the table width), as fp32 partials and the combine. Sizes only: a
-    graph-captured launch keeps its grid."""
+    """``policy_splits`` for a launch's tensors (1 for an empty batch or CPU tensors,
+    whose launch raises)."""
     b, hq, d = q.shape
-    if b == 0 or not q.is_cuda:  # nothing to launch, or the launch raises
+    if b == 0 or not q.is_cuda:
         return 1
-    hkv, width = k_cache.shape[1], block_tables.shape[1]
-    splits = num_splits_for(b, hkv, width)
-    waves = _one_split_waves(q.device.index, b, hq, hkv, d, block_size, width, q.dtype)
-    if waves >= IN_GROUP_MIN_WAVES // 2:
-        return 1 if splits <= IN_GROUP_SPLITS else splits
-    return max(splits, min(-(-2 * IN_GROUP_MIN_WAVES // max(waves, 1)), MAX_SPLITS, width))
+    return policy_splits(b, hq, k_cache.shape[1], d, block_size, block_tables.shape[1], q.dtype,
+                         q.device.index)  # fmt: skip
 
 
 def _launch(
@@ -360,7 +369,7 @@ def launch_paged_decode_split(
     the states stay in each workgroup's LDS and the merge runs in the same launch;
     smaller grids, and block sizes under a loop iteration's tokens, write fp32 partials
     to HBM and combine them in a second launch. Without a count, it comes
-    from ``_policy_splits``: ``num_splits_for(B, Hkv, max_blocks)``, where a count up to
+    from ``policy_splits``: ``num_splits_for(B, Hkv, max_blocks)``, where a count up to
     ``IN_GROUP_SPLITS`` becomes one launch whose workgroups split each sequence over
     their waves (the library sizes the workgroup to the grid), raised for grids too
     small to fill the chip."""
