@@ -213,6 +213,33 @@ def hbm_split_combine(g: DecodeCase, splits: int) -> torch.Tensor:
     return out
 
 
+def in_group_split(g: DecodeCase, splits: int) -> torch.Tensor:
+    """ts_decode_split with no partial buffers: the split ranges merge in each workgroup."""
+    b, hq, d = g.q.shape
+    out = torch.empty_like(g.q)
+    _lib.call("ts_decode_split", g.q.data_ptr(), g.k_cache.data_ptr(), g.v_cache.data_ptr(),
+              g.block_tables.data_ptr(), g.context_lens.data_ptr(), out.data_ptr(), None, None,
+              None, b, hq, g.k_cache.shape[1], d, g.block_size, g.q.stride(0), g.q.stride(1),
+              out.stride(0), out.stride(1), g.k_cache.stride(0), g.k_cache.stride(1),
+              g.block_tables.stride(0), g.block_tables.shape[1], splits, 0, g.scale,
+              _lib.dtype_code(g.q), _lib.stream_of(0))  # fmt: skip
+    return out
+
+
+@pytest.mark.parametrize("splits", [56, 60, 100])
+def test_in_group_splits_past_one_wave_of_slots(splits: int) -> None:
+    # The C ABI takes any split count whose states fit the workgroup's LDS. With small
+    # states (64-element rows, one query head per kv head) the split ranges plus the
+    # waves' pieces can exceed 64 slots per sequence; every slot must still be merged.
+    c = decode_case([3000, 1500, 4096, 77], num_q_heads=4, num_kv_heads=4, head_dim=64,
+                    dtype=torch.float16, seed=9)
+    want = oracle32(c)
+    g = on_gpu(c)
+    out = in_group_split(g, splits)
+    torch.cuda.synchronize()
+    assert_contract(out, want, torch.float16, f"in-group {splits} splits, D=64")
+
+
 def test_baseline_config_2() -> None:
     # BASELINE config 2: fp16, B=32 at context 256, a 4096-block pool, 4 splits: the
     # reference's ranges of ceil(16 / 4) = 4 blocks, each with its own softmax state, merged

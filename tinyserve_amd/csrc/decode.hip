@@ -654,10 +654,11 @@ void paged_attend_kernel(const AttendArgs a) {
       const int g = (t % (HT * D)) / D, d = t % D;
       const int s0 = pi * nsl;
       float den = 0.f, num = 0.f;
-      if constexpr (D % kWave == 0) {
+      if (D % kWave == 0 && nsl <= kWave) {
         // A wave's 64 outputs share (sequence, head): lane s takes slot s's maximum and
         // denominator, the wave forms every slot's weight at once (one exponential per
-        // lane), and the weights are broadcast slot by slot for the accumulators.
+        // lane), and the weights are broadcast slot by slot for the accumulators. (More
+        // than 64 slots, possible at small states, take the loop below.)
         // An unused slot has only its maximum written: its other fields are never read.
         const float ms = lane < nsl ? ss.m(s0 + lane, g) : kNoMax;
         const float ls = ms != kNoMax ? ss.l(s0 + lane, g) : 0.f;
