@@ -188,14 +188,16 @@ __device__ __forceinline__ void ring_barrier() {
 }
 
 template <typename T, int D, int HG, int QB, int kWaves, int kStages, int kBN, int kOcc,
-          bool kScalarIds, bool kSplitK>
+          bool kScalarIds, int kParts>
 __global__ __launch_bounds__(kWaves * kWave) __attribute__((amdgpu_waves_per_eu(kOcc, kOcc))) void
 prefill_mfma_kernel(const PrefillArgs a) {
   using V8 = typename Mfma<T>::V8;
-  // Key split: waves w and w + kWaves / 2 take the same queries and heads; the first
-  // walks the lower half of the workgroup's key tiles, the second the upper half, and
-  // the two softmax states are merged through LDS at the end. kGW waves share a tile.
-  constexpr int kGW = kSplitK ? kWaves / 2 : kWaves;
+  // Key split (kParts > 1): waves w, w + kGW, ... take the same queries and heads; part
+  // kh walks the kh-th contiguous share of the workgroup's key tiles, and the parts'
+  // softmax states are merged through LDS at the end. kGW waves share a tile.
+  constexpr bool kSplitK = kParts > 1;
+  constexpr int kGW = kWaves / kParts;
+  static_assert(kGW * kParts == kWaves, "whole waves per key part");
   static_assert(!kSplitK || (kScalarIds && kStages == 2), "key split: scalar ids, 2 stages");
   using Sh = TileShape<D, kGW, kBN>;
   constexpr int NH = kBN / 32;  // 32-key halves of S^T (one MFMA accumulator each)
@@ -213,7 +215,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
   // and P.V takes two MFMAs. fp16's 11 bits meet the tolerance with one.
   constexpr bool kSplitP = std::is_same_v<T, bf16>;
 
-  constexpr int kStageStride = (kSplitK ? 2 : 1) * TILE;  // one tile per key half
+  constexpr int kStageStride = kParts * TILE;  // one tile per key part
   __shared__ __attribute__((aligned(16))) T k_ring[kStages * kStageStride];
   __shared__ __attribute__((aligned(16))) T v_ring[kStages * kStageStride];
   __shared__ int32_t ids_lds[kWin];
@@ -221,8 +223,8 @@ prefill_mfma_kernel(const PrefillArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kh = kSplitK ? wave / kGW : 0;           // key half
-  const int wl = kSplitK ? wave - kh * kGW : wave;  // wave within its half
+  const int kh = kSplitK ? wave / kGW : 0;           // key part
+  const int wl = kSplitK ? wave - kh * kGW : wave;  // wave within its part
   const int col = lane & 31;  // this lane's query within the wave's 32
   const int half = lane >> 5;
 
@@ -591,7 +593,7 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
     if (n0 < wave_key_end) attend(k_cur, v_cur, n0);
   };
-  // Stage s of this wave's key half: one tile, at (s * halves + kh) tiles.
+  // Stage s of this wave's key part: one tile, at (s * kParts + kh) tiles.
   T* const k0 = k_ring + kh * TILE;
   T* const v0 = v_ring + kh * TILE;
   T* const k1 = k0 + kStageStride;
@@ -604,12 +606,13 @@ prefill_mfma_kernel(const PrefillArgs a) {
     __syncthreads();
   }
   if constexpr (kSplitK) {
-    // The lower half takes tiles 0 .. n_lo - 1, the upper half the rest; both step n_lo
-    // times (the same barriers), the upper half's last step possibly with no tile.
+    // Part kh takes tiles kh * n_lo .. (kh + 1) * n_lo - 1 (the last part the rest); all
+    // parts step n_lo times (the same barriers), later parts' last steps possibly with no
+    // tile.
     const int ntiles = (key_end + kBN - 1) / kBN;
-    const int n_lo = (ntiles + 1) / 2;
+    const int n_lo = (ntiles + kParts - 1) / kParts;
     const int base = kh * n_lo * kBN;
-    const int half_end = kh ? key_end : min(n_lo * kBN, key_end);
+    const int half_end = kh == kParts - 1 ? key_end : min((kh + 1) * n_lo * kBN, key_end);
     auto sstep = [&](const T* k_cur, const T* v_cur, T* k_nx, T* v_nx, int n0) {
       ring_barrier<0>();
       if (n0 + kBN < half_end) gather(k_nx, v_nx, n0 + kBN);
@@ -644,35 +647,44 @@ prefill_mfma_kernel(const PrefillArgs a) {
   __builtin_amdgcn_s_waitcnt(0x0070);
 
   if constexpr (kSplitK) {
-    // Merge the upper half's state into the lower half's, lane by lane (the two waves
-    // have the same layout): m, l and O^T[0] through k_ring, O^T[1..] through v_ring,
-    // lane-fastest so that the accesses are conflict-free. Scores are in base-2 units.
-    __syncthreads();  // every wave is done with the ring
+    // Merge every later part's state into part 0's, lane by lane (the waves have the same
+    // layout), one part at a time: m, l and O^T[0] through k_ring, O^T[1..] through
+    // v_ring, lane-fastest so that the accesses are conflict-free. Scores are in base-2
+    // units.
+    static_assert(kGW * (2 + 16) * kWave * 4 <= sizeof(k_ring), "parked m, l, O^T[0] fit");
+    static_assert(kGW * (DT - 1) * 16 * kWave * 4 <= sizeof(v_ring), "parked O^T[1..] fit");
     float* xk = reinterpret_cast<float*>(k_ring) + wl * (2 + 16) * kWave + lane;
     float* xv = reinterpret_cast<float*>(v_ring) + wl * (DT - 1) * 16 * kWave + lane;
-    if (kh == 1) {
-      xk[0] = m_run;
-      xk[kWave] = l_run;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) xk[(2 + e) * kWave] = oacc[0][e];
+    for (int part = kParts - 1; part >= 1; --part) {
+      __syncthreads();  // every wave is done with the ring (or with the previous merge)
+      if (kh == part) {
+        xk[0] = m_run;
+        xk[kWave] = l_run;
 #pragma unroll
-      for (int dt = 1; dt < DT; ++dt)
+        for (int e = 0; e < 16; ++e) xk[(2 + e) * kWave] = oacc[0][e];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) xv[((dt - 1) * 16 + e) * kWave] = oacc[dt][e];
+        for (int dt = 1; dt < DT; ++dt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) xv[((dt - 1) * 16 + e) * kWave] = oacc[dt][e];
+      }
+      __syncthreads();
+      if (kh == 0) {
+        const float m1 = xk[0];
+        const float mn = fmaxf(m_run, m1);
+        const float a0 = fast_exp2(m_run - mn), a1 = fast_exp2(m1 - mn);
+        l_run = l_run * a0 + xk[kWave] * a1;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[0][e] = oacc[0][e] * a0 + xk[(2 + e) * kWave] * a1;
+#pragma unroll
+        for (int dt = 1; dt < DT; ++dt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            oacc[dt][e] = oacc[dt][e] * a0 + xv[((dt - 1) * 16 + e) * kWave] * a1;
+        m_run = mn;
+      }
     }
-    __syncthreads();
-    if (kh == 1) return;
-    const float m1 = xk[0];
-    const float mn = fmaxf(m_run, m1);
-    const float a0 = fast_exp2(m_run - mn), a1 = fast_exp2(m1 - mn);
-    l_run = l_run * a0 + xk[kWave] * a1;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) oacc[0][e] = oacc[0][e] * a0 + xk[(2 + e) * kWave] * a1;
-#pragma unroll
-    for (int dt = 1; dt < DT; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) oacc[dt][e] = oacc[dt][e] * a0 + xv[((dt - 1) * 16 + e) * kWave] * a1;
-    m_run = mn;
+    if (kh != 0) return;
   }
 
   const float l_tot = halves_sum(l_run);
@@ -692,23 +704,23 @@ prefill_mfma_kernel(const PrefillArgs a) {
     }
 }
 
-// SPLIT: the key-split shape (W waves, W / 2 per key half); its caller checks that the
+// KP > 1: the key-split shape (W waves, W / KP per key part); its caller checks that the
 // block size allows the scalar-id gather.
-template <typename T, int D, int HG, int W, int S, int BN, int OCC, bool SPLIT = false>
+template <typename T, int D, int HG, int W, int S, int BN, int OCC, int KP = 1>
 static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream) {
-  constexpr int QB = (SPLIT ? W / 2 : W) / HG;
+  constexpr int QB = W / KP / HG;
   const int seqs = a.seq_group > 0 ? (a.R + a.seq_group - 1) / a.seq_group * a.seq_group : a.R;
   dim3 grid(static_cast<unsigned>(a.n_qtiles) * seqs * Hkv * a.hchunks);
-  if constexpr (SPLIT) {
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, true, true>), grid,
+  if constexpr (KP > 1) {
+    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, true, KP>), grid,
                        dim3(W * kWave), 0, stream, a);
-    return launch_status();
+  } else {
+    // A load's RPI rows share a cache block when blocks hold at least RPI slots.
+    if ((1 << a.lbs) >= TileShape<D, W, BN>::kRPI)
+      hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, true, 1>), grid, dim3(W * kWave), 0, stream, a);
+    else
+      hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, false, 1>), grid, dim3(W * kWave), 0, stream, a);
   }
-  // A load's RPI rows share a cache block when blocks hold at least RPI slots.
-  if ((1 << a.lbs) >= TileShape<D, W, BN>::kRPI)
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, true, false>), grid, dim3(W * kWave), 0, stream, a);
-  else
-    hipLaunchKernelGGL((prefill_mfma_kernel<T, D, HG, QB, W, S, BN, OCC, false, false>), grid, dim3(W * kWave), 0, stream, a);
   return launch_status();
 }
 
@@ -716,9 +728,9 @@ static int launch_prefill_mfma(const PrefillArgs& a, int Hkv, hipStream_t stream
 // work; the 4-wave shape halves the work per workgroup and fits two workgroups per CU,
 // which wins when the launch has fewer than two 8-wave workgroups per CU (e.g. one
 // 2048-token prompt: 128 workgroups of 8 waves).
-template <typename T, int D, int W, int S, int BN, int OCC, bool SPLIT = false>
+template <typename T, int D, int W, int S, int BN, int OCC, int KP = 1>
 static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows, hipStream_t stream) {
-  constexpr int WQ = SPLIT ? W / 2 : W;  // waves over the queries and heads
+  constexpr int WQ = W / KP;  // waves over the queries and heads
   const int hg = a.group < WQ ? a.group : WQ;
   a.hchunks = a.group / hg;
   const int bq = 32 * (WQ / hg);
@@ -744,13 +756,13 @@ static int dispatch_hg_w(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows,
     }
   }
   switch (hg) {
-    case 1: return launch_prefill_mfma<T, D, 1, W, S, BN, OCC, SPLIT>(a, Hkv, stream);
-    case 2: return launch_prefill_mfma<T, D, 2, W, S, BN, OCC, SPLIT>(a, Hkv, stream);
+    case 1: return launch_prefill_mfma<T, D, 1, W, S, BN, OCC, KP>(a, Hkv, stream);
+    case 2: return launch_prefill_mfma<T, D, 2, W, S, BN, OCC, KP>(a, Hkv, stream);
     case 4:
-      if constexpr (WQ >= 4) return launch_prefill_mfma<T, D, 4, W, S, BN, OCC, SPLIT>(a, Hkv, stream);
+      if constexpr (WQ >= 4) return launch_prefill_mfma<T, D, 4, W, S, BN, OCC, KP>(a, Hkv, stream);
       return TS_EUNSUPPORTED;
     case 8:
-      if constexpr (WQ >= 8) return launch_prefill_mfma<T, D, 8, W, S, BN, OCC, SPLIT>(a, Hkv, stream);
+      if constexpr (WQ >= 8) return launch_prefill_mfma<T, D, 8, W, S, BN, OCC, KP>(a, Hkv, stream);
       return TS_EUNSUPPORTED;
     default: return TS_EUNSUPPORTED;
   }
@@ -792,7 +804,7 @@ static int dispatch_hg(PrefillArgs& a, int Hkv, int max_q_len, int64_t n_rows, h
       // Two key halves per workgroup (8 waves, one workgroup and two waves per SIMD per
       // CU) where the scalar-id gather applies; else the plain 4-wave shape.
       if ((1 << a.lbs) >= TileShape<D, 4, 64>::kRPI)
-        return dispatch_hg_w<T, D, 8, 2, 64, 2, true>(a, Hkv, max_q_len, n_rows, stream);
+        return dispatch_hg_w<T, D, 8, 2, 64, 2, 2>(a, Hkv, max_q_len, n_rows, stream);
       return dispatch_hg_w<T, D, 4, 2, 64, 2>(a, Hkv, max_q_len, n_rows, stream);
     default: return dispatch_hg_w<T, D, 8, 3, 64, 2>(a, Hkv, max_q_len, n_rows, stream);
   }
